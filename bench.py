@@ -1,0 +1,197 @@
+"""Benchmark: CA cell-updates/s of the multi-head neural-CA step on one MI355X.
+
+Workload ("c3"): 128x128 toroidal grid, 8 heads, head_dim 64,
+batch 64, bf16 state and weights with fp32 accumulation, synthetic seeded input
+resident in HBM. One step = S1 projections ([P|I|V] GEMM, 1,048,576 x 512 x 1536)
++ the fused stencil (S2-S6) + mass conservation (S7) over the whole batch; one
+cell-update = one (batch, y, x) cell advanced one step across all 8 heads x 64
+channels. The timed region is a single slime_ca_step call of K steps.
+
+Prints one JSON line. ``roofline`` describes the dominant kernel, measured with
+HIP events on the library's stream in a second pass of K steps;
+``cpu_baseline`` times the CPU oracle on a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "CA cell-updates/s (128², 8 heads, d=64) on 1 MI355X; % HBM / MFMA peak"
+PEAK_HBM_GBS = 8000.0        # MI355X HBM3E
+PEAK_TFLOPS = {"bf16": 2500.0, "fp32": 157.3}  # dense MFMA
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def stencil_bytes_per_cell(cfg) -> int:
+    """Algorithmic HBM bytes of the fused stencil per cell-update: read X, P, I, V
+    and write Y once (C channels each), plus per-cell mu, sigma when present."""
+    elem = 2 if cfg.dtype == "bf16" else 4
+    return 5 * cfg.C * elem + (2 * cfg.H * 4 if cfg.growth_per_cell else 0)
+
+
+def gemm_flops_per_cell(cfg) -> int:
+    """2 * C * 3C multiply-adds per cell for the fused [P|I|V] projection."""
+    return 2 * cfg.C * 3 * cfg.C
+
+
+def load_traffic(kernel: str, workload: str):
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE),
+    committed under profiles/; None when no measurement is committed."""
+    path = os.path.join(ROOT, "profiles", "pmc_traffic.json")
+    try:
+        with open(path) as f:
+            data = json.load(f)
+        return data.get(workload, {}).get(kernel, {}).get("bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_baseline(cfg, params, X, seconds: float):
+    import numpy as np
+
+    import oracle
+    from slime_amd import round_bf16
+    ocfg = oracle.OracleConfig(B=1, G=cfg.G, H=cfg.H, D=cfg.D, pods=1,
+                               growth_per_cell=cfg.growth_per_cell, dt=cfg.dt)
+    p = {k: (round_bf16(v[:1]) if k in ("WP", "WI", "WV") else v[:1]) for k, v in params.items()}
+    x1 = np.ascontiguousarray(X[0:1])
+    oracle.step(ocfg, x1, p, 1)  # warm-up (page-in, thread pool)
+    n, t = 0, 0.0
+    while t < seconds and n < 50:
+        t0 = time.perf_counter()
+        oracle.step(ocfg, x1, p, 1)
+        t += time.perf_counter() - t0
+        n += 1
+    cells = cfg.G * cfg.G
+    return {
+        "value": cells * n / t,
+        "unit": "cell-updates/s",
+        "cores": oracle.num_threads(),
+        "kind": "port",
+        "sample": f"CPU oracle (fp64, OpenMP) on batch entry 0 of the same workload: "
+                  f"{n} step(s) of {cells} cells in {t:.1f} s",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--config", default="c3")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported in this "
+              "build (the path shards by batch with no collective; see DESIGN.md)",
+              file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    from slime_amd import CONFIGS, Pseudopod, make_params, make_state
+
+    cfg = CONFIGS[args.config]
+    log(f"config {cfg}")
+    params = make_params(cfg, seed=1)
+    X = make_state(cfg, seed=2)
+    tdt = torch.bfloat16 if cfg.dtype == "bf16" else torch.float32
+    x = torch.from_numpy(X).to("cuda").to(tdt).contiguous()
+    y = torch.empty_like(x)
+    K, W = args.steps, args.warmup
+    cells = cfg.cell_updates_per_step
+
+    with Pseudopod(cfg.B, cfg.G, cfg.H, cfg.D, cfg.dtype, cfg.dt, cfg.growth_per_cell,
+                   cfg.pods) as ca:
+        ca.set_params(params)
+        log(f"MFMA projection path: {ca.uses_mfma}")
+        if W > 0:
+            ca.forward(x, out=y, n_steps=W)
+        torch.cuda.synchronize()
+        log("warmup done")
+
+        # ---- timed region: exactly K steps ------------------------------------------
+        stream = torch.cuda.current_stream()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ev0.record(stream)
+        ca.forward(x, out=y, n_steps=K)
+        ev1.record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        dev_ms = ev0.elapsed_time(ev1)
+        log(f"timed {K} steps: {wall * 1e3:.2f} ms wall, {dev_ms:.2f} ms device")
+        mass_in, mass_out = ca.mass()
+        drift = float(np.max(np.abs(mass_out - mass_in) / np.abs(mass_in)))
+        finite = bool(torch.isfinite(y.float()).all())
+
+        # ---- per-kernel durations (HIP events on the library's stream) ----------------
+        ca.set_timing(True)
+        ca.forward(x, out=y, n_steps=K)
+        t = ca.timings()
+        ca.set_timing(False)
+
+    ms_per_step = wall * 1e3 / K
+    value = cells * K / wall
+    gemm_ms = t["gemm_ms"] / max(t["gemm_launches"], 1)
+    sten_ms = t["stencil_ms"] / max(t["stencil_launches"], 1)
+    sb = stencil_bytes_per_cell(cfg) * cells
+    gf = gemm_flops_per_cell(cfg) * cells
+    wl = f"{cfg.name}"
+    kernels = {
+        "stencil": {"bound": "hbm", "achieved": sb / (sten_ms * 1e-3) / 1e9, "peak": PEAK_HBM_GBS,
+                    "unit": "GB/s", "avg_ms": sten_ms, "algorithmic_bytes": sb,
+                    "traffic": load_traffic("stencil", wl)},
+        "projection_gemm": {"bound": "mfma", "achieved": gf / (gemm_ms * 1e-3) / 1e12,
+                            "peak": PEAK_TFLOPS[cfg.dtype], "unit": "TFLOP/s", "avg_ms": gemm_ms,
+                            "algorithmic_flops": gf, "traffic": load_traffic("gemm", wl)},
+    }
+    for k in kernels.values():
+        k["frac"] = k["achieved"] / k["peak"]
+    dom_name = "stencil" if sten_ms >= gemm_ms else "projection_gemm"
+    dom = kernels[dom_name]
+    roofline = {"kernel": dom_name, "bound": dom["bound"], "achieved": dom["achieved"],
+                "peak": dom["peak"], "unit": dom["unit"], "frac": dom["frac"],
+                "traffic": dom["traffic"]}
+    log(f"stencil {sten_ms:.3f} ms ({kernels['stencil']['frac']:.1%} of HBM), gemm {gemm_ms:.3f} ms "
+        f"({kernels['projection_gemm']['frac']:.1%} of MFMA)")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("timing the CPU oracle baseline")
+        cpu = cpu_baseline(cfg, params, X, args.cpu_seconds)
+
+    out = {
+        "metric": METRIC, "value": value, "unit": "cell-updates/s", "n_gpus": 1, "steps": K,
+        "warmup": W, "ms_per_step": ms_per_step, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": cfg.dtype,
+        "data": "synthetic: seeded U[0,1) state with 5% blobs, N(0,0.05) weights, "
+                "mu~U[0.1,0.3], sigma~U[0.01,0.05]",
+        "config": {"workload": f"{cfg.name}: {cfg.G}x{cfg.G} toroidal grid, {cfg.H} heads, "
+                               f"head_dim {cfg.D}, batch {cfg.B}, {cfg.dtype}, "
+                               f"{K} steps per call",
+                   "grid": cfg.G, "heads": cfg.H, "head_dim": cfg.D, "batch": cfg.B,
+                   "steps_per_call": K, "parallelism": "single GPU"},
+        "device_ms_per_step": dev_ms / K,
+        "mass_drift_max": drift, "finite": finite,
+        "roofline": roofline, "kernels": kernels, "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,145 @@
+/*
+ * slime_ca.h — C ABI of the MI355X (gfx950) multi-head neural-CA step.
+ *
+ * Drop-in for the CA hot path of J0pari/Slime. Each entry point names the
+ * reference interface it replaces (paths under the reference tree):
+ *
+ *   slime_ca_create / slime_ca_destroy      buffer ownership of create_organism /
+ *                                           destroy_organism for the CA state
+ *                                           (slime/runtime.cu:66-94,173-182,453-461)
+ *   slime_ca_set_params                     init_multihead_ca_kernel
+ *                                           (slime/core/pseudopod.cu:386-444)
+ *   slime_ca_project                        multi_head_ca_kernel
+ *                                           (slime/core/pseudopod.cu:41-49)
+ *   slime_ca_flow_lenia                     flow_lenia_dynamics_kernel + mix_heads_kernel
+ *                                           (slime/core/pseudopod.cu:134-141,217-223)
+ *   slime_ca_step                           the CA part of neural_ca_update_kernel
+ *                                           (slime/core/organism.cu:639-669)
+ *   slime_ca_mass                           mass_buffer (slime/core/pseudopod.cu:35,205-213)
+ *   slime_ca_fitness                        fitness_fused_kernel
+ *                                           (slime/kernels/warp_ca.cu:178-226)
+ *   slime_ca_init_from_field /
+ *   slime_ca_field_from_state               initialize_ca_from_field_kernel /
+ *                                           update_field_from_ca_kernel
+ *                                           (slime/core/organism.cu:691-743)
+ *   slime_ca_last_error                     the printed message of CUDA_CHECK
+ *                                           (slime/runtime.cu:11-20), returned instead
+ *                                           of exit(1)
+ *
+ * Conventions
+ *   - Every function returns SLIME_OK (0) or a negative SLIME_E* code and never
+ *     exits the process; slime_ca_last_error() describes the last failure on the
+ *     calling thread.
+ *   - State tensors are device pointers, channels-last [B][G][G][C] with
+ *     C = H * D, element type = the handle's dtype (fp32, or bf16 as raw 16-bit
+ *     words). Arithmetic is fp32 (fp64 for reductions and the Jacobi solve).
+ *   - Parameters are host fp32 arrays, row-major:
+ *       WP, WI, WV   [pods][C][C]   row k = input channel, column n = output channel
+ *       K            [pods][H][9]   tap k = 3*(dy+1)+(dx+1), toroidal neighbours
+ *       mu, sigma    [pods][H], or [pods][G][G][H] when growth_per_cell = 1
+ *       M            [pods][H][H]   M[o][h]: weight of head h in output head o
+ *     Batch entry b uses parameter set b / (B / pods).
+ *   - stream is a hipStream_t passed as void* (NULL = default stream). Calls on
+ *     one handle are stream-ordered and not thread-safe; use one stream per
+ *     handle. No HIP types appear in this header.
+ */
+#ifndef SLIME_CA_H
+#define SLIME_CA_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SLIME_OK 0
+#define SLIME_EINVAL (-1)  /* invalid argument or configuration */
+#define SLIME_ENOMEM (-2)  /* device allocation failed */
+#define SLIME_EHIP (-3)    /* HIP runtime error */
+#define SLIME_ENODEV (-4)  /* no usable gfx950 device */
+#define SLIME_ESTATE (-5)  /* call out of order (e.g. step before set_params) */
+
+#define SLIME_F32 0
+#define SLIME_BF16 1
+
+typedef struct slime_ca slime_ca;
+
+typedef struct {
+    int B;               /* batch entries */
+    int G;               /* grid side (toroidal), multiple of 8, >= 8 */
+    int H;               /* heads, must be 8 (NUM_HEADS, slime/core/pseudopod.cu:15) */
+    int D;               /* head dim: 8, 16, 32 or 64 */
+    int dtype;           /* SLIME_F32 or SLIME_BF16: storage of state and weights */
+    float dt;            /* update step, 0.1 in the reference (slime/core/organism.cu:659) */
+    int growth_per_cell; /* 0: mu, sigma per head; 1: per cell and head */
+    int pods;            /* independent parameter sets; B % pods == 0 */
+    int pvi_chain;       /* 0: P, I, V all from X; 1: I from P and V from I
+                            (the chained form of slime/core/pseudopod.cu:98-119) */
+} slime_ca_config;
+
+typedef struct {
+    const float* WP;
+    const float* WI;
+    const float* WV;
+    const float* K;
+    const float* mu;
+    const float* sigma;
+    const float* M;
+} slime_ca_params;
+
+/* Allocates every device buffer the step needs on the current device. */
+int slime_ca_create(const slime_ca_config* config, slime_ca** out);
+int slime_ca_destroy(slime_ca* ca);
+
+/* Uploads parameters (host fp32, layouts above). Synchronous. */
+int slime_ca_set_params(slime_ca* ca, const slime_ca_params* params);
+
+/* S1: P = ReLU(X W_P), I = GELU_tanh(X W_I) (or of P W_I when chained),
+ * V = X W_V (or I W_V). P, I, V are [B][G][G][C] in the handle's dtype. */
+int slime_ca_project(slime_ca* ca, const void* x_in, void* P, void* I, void* V, void* stream);
+
+/* S2-S7 on given projections: 3x3 toroidal potential, bell growth, 3x3 CA
+ * activation, value propagation, modulated update, head mixing and per-(b, head)
+ * mass conservation. y_out must not alias x_in, P, I or V. */
+int slime_ca_flow_lenia(slime_ca* ca, const void* x_in, const void* P, const void* I,
+                        const void* V, void* y_out, void* stream);
+
+/* n_steps full steps S1-S7 from x_in to x_out (x_out may equal x_in). After the
+ * call the handle's mass buffer holds the last step's per-(b, head) sums. */
+int slime_ca_step(slime_ca* ca, const void* x_in, void* x_out, int n_steps, void* stream);
+
+/* Host copies of the last step's per-(b, head) input mass and output mass
+ * (after conservation), B*H doubles each. Synchronises the last stream used. */
+int slime_ca_mass(slime_ca* ca, double* h_mass_in, double* h_mass_out);
+
+/* E1-E5 over a device history [T][B][G][G][C] (2 <= T <= 65): per (b, head)
+ * effective rank of the last state's Gram matrix (64x64 Jacobi for D = 64),
+ * lag-1 coherence over the T states and their product. Outputs are device
+ * float arrays of B*H entries. */
+int slime_ca_fitness(slime_ca* ca, const void* x_hist, int T, float* erank, float* coherence,
+                     float* fitness, void* stream);
+
+/* Jacobi sweeps used by the last slime_ca_fitness call, B*H ints (host copy). */
+int slime_ca_fitness_sweeps(slime_ca* ca, int* h_sweeps);
+
+/* Organism adapters for one G x G grid of C channels in the handle's dtype:
+ * X[y][x][c] = conc[y][x] * sin(0.1 c), and conc[y][x] = mean_c X[y][x][c]. */
+int slime_ca_init_from_field(slime_ca* ca, const float* conc, void* x, void* stream);
+int slime_ca_field_from_state(slime_ca* ca, const void* x, float* conc, void* stream);
+
+/* Kernel timing (no counterpart in the reference, which has no timers on this
+ * path). While enabled, slime_ca_step records HIP events on its stream around
+ * each projection GEMM and each fused stencil launch; slime_ca_timings returns
+ * the summed device milliseconds and launch counts since timing was enabled
+ * (it synchronises the last stream used). Enabling resets the sums. */
+int slime_ca_set_timing(slime_ca* ca, int enable);
+int slime_ca_timings(slime_ca* ca, double* gemm_ms, int* gemm_launches, double* stencil_ms,
+                     int* stencil_launches);
+
+/* 1 when this build runs S1 on the MFMA tile kernel for the handle's shape. */
+int slime_ca_uses_mfma(const slime_ca* ca);
+
+const char* slime_ca_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SLIME_CA_H */

@@ -1,0 +1,544 @@
+// api.cpp — the C ABI declared in include/slime_ca.h: handle ownership,
+// argument validation and the host-ordered launch sequence of one CA step.
+//
+// The reference orchestrates the step from the device with dynamic parallelism
+// (neural_ca_update_kernel, slime/core/organism.cu:617-688) and aborts the
+// process on any CUDA error (CUDA_CHECK, slime/runtime.cu:11-20). Here the host
+// enqueues the kernels on the caller's stream and every failure becomes a
+// status code plus a thread-local message.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/slime_ca.h"
+#include "kernels.hpp"
+
+using namespace slime;
+
+struct slime_ca {
+    slime_ca_config cfg;
+    int C = 0;
+    int tiles = 0;
+    int device = 0;
+    size_t elem = 4;
+    long long state_elems = 0;
+    bool params_set = false;
+    hipStream_t last_stream = nullptr;
+
+    float* W = nullptr;        // [pods][3][C][C] fp32 masters
+    void* Wt = nullptr;        // [B][3C][C] per-batch scaled, transposed
+    float* K = nullptr;        // [pods][H][9]
+    float* mu = nullptr;       // [pods][H] or [pods][G][G][H]
+    float* sigma = nullptr;
+    float* M = nullptr;        // [pods][H][H]
+    void* P = nullptr;         // [B][G][G][C] work buffers for slime_ca_step
+    void* I = nullptr;
+    void* V = nullptr;
+    void* S[2] = {nullptr, nullptr};  // unscaled step outputs (ping-pong)
+    float* part_in = nullptr;  // [B*H][tiles]
+    float* part_out = nullptr;
+    float* scale[2] = {nullptr, nullptr};  // [B*H]
+    float* unit_scale = nullptr;           // [B*H] of 1.0
+    double* mass_in = nullptr;             // [B*H]
+    double* mass_out = nullptr;
+
+    int fit_chunks = 0;
+    int fit_T = 0;             // history length the fitness partials are sized for
+    float* gram_part = nullptr;
+    float* mom_part = nullptr;
+    int* sweeps = nullptr;     // [B*H]
+
+    // Optional per-kernel timing: event pairs recorded around launches.
+    bool timing = false;
+    std::vector<hipEvent_t> ev_pool;
+    size_t ev_used = 0;
+    std::vector<std::pair<size_t, size_t>> gemm_ev, stencil_ev;
+};
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+#define HIP_TRY(expr)                                                                         \
+    do {                                                                                      \
+        hipError_t e_ = (expr);                                                               \
+        if (e_ != hipSuccess)                                                                 \
+            return fail(e_ == hipErrorOutOfMemory ? SLIME_ENOMEM : SLIME_EHIP, "%s: %s (%s:%d)", \
+                        #expr, hipGetErrorString(e_), __FILE__, __LINE__);                    \
+    } while (0)
+
+int dalloc(void** p, size_t bytes) {
+    *p = nullptr;
+    if (bytes == 0) return SLIME_OK;
+    hipError_t e = hipMalloc(p, bytes);
+    if (e != hipSuccess) {
+        *p = nullptr;
+        return fail(SLIME_ENOMEM, "hipMalloc(%zu bytes): %s", bytes, hipGetErrorString(e));
+    }
+    return SLIME_OK;
+}
+
+template <typename P>
+int dalloc_t(P** p, size_t bytes) {
+    void* v = nullptr;
+    int rc = dalloc(&v, bytes);
+    *p = static_cast<P*>(v);
+    return rc;
+}
+
+int validate(const slime_ca_config* c) {
+    if (!c) return fail(SLIME_EINVAL, "config is NULL");
+    if (c->B < 1) return fail(SLIME_EINVAL, "B=%d must be >= 1", c->B);
+    if (c->G < 8 || c->G % 8 != 0) return fail(SLIME_EINVAL, "G=%d must be a multiple of 8", c->G);
+    if (c->H != kHeads) return fail(SLIME_EINVAL, "H=%d unsupported (must be %d)", c->H, kHeads);
+    if (c->D != 8 && c->D != 16 && c->D != 32 && c->D != 64)
+        return fail(SLIME_EINVAL, "D=%d unsupported (8, 16, 32 or 64)", c->D);
+    if (c->dtype != SLIME_F32 && c->dtype != SLIME_BF16)
+        return fail(SLIME_EINVAL, "dtype=%d unsupported", c->dtype);
+    if (c->pods < 1 || c->B % c->pods != 0)
+        return fail(SLIME_EINVAL, "pods=%d must divide B=%d", c->pods, c->B);
+    if (!std::isfinite(c->dt)) return fail(SLIME_EINVAL, "dt is not finite");
+    if (c->growth_per_cell != 0 && c->growth_per_cell != 1)
+        return fail(SLIME_EINVAL, "growth_per_cell must be 0 or 1");
+    if (c->pvi_chain != 0 && c->pvi_chain != 1) return fail(SLIME_EINVAL, "pvi_chain must be 0 or 1");
+    const double elems = (double)c->B * c->G * c->G * c->H * c->D;
+    if (elems > 4.0e9) return fail(SLIME_EINVAL, "state of %.3g elements is too large", elems);
+    return SLIME_OK;
+}
+
+hipEvent_t next_event(slime_ca* h) {
+    if (h->ev_used == h->ev_pool.size()) {
+        hipEvent_t e = nullptr;
+        if (hipEventCreate(&e) != hipSuccess) return nullptr;
+        h->ev_pool.push_back(e);
+    }
+    return h->ev_pool[h->ev_used++];
+}
+
+// Records an event pair around the launches in fn when timing is enabled.
+template <typename Fn>
+hipError_t timed(slime_ca* h, std::vector<std::pair<size_t, size_t>>& log, hipStream_t s, Fn fn) {
+    if (!h->timing) return fn();
+    hipEvent_t a = next_event(h);
+    const size_t ia = h->ev_used - 1;
+    hipEvent_t b = next_event(h);
+    const size_t ib = h->ev_used - 1;
+    if (!a || !b) return hipErrorOutOfMemory;
+    hipError_t e = hipEventRecord(a, s);
+    if (e == hipSuccess) e = fn();
+    if (e == hipSuccess) e = hipEventRecord(b, s);
+    if (e == hipSuccess) log.emplace_back(ia, ib);
+    return e;
+}
+
+void release(slime_ca* h) {
+    for (hipEvent_t e : h->ev_pool) (void)hipEventDestroy(e);
+    h->ev_pool.clear();
+    void* ptrs[] = {h->W, h->Wt, h->K, h->mu, h->sigma, h->M, h->P, h->I, h->V, h->S[0], h->S[1],
+                    h->part_in, h->part_out, h->scale[0], h->scale[1], h->unit_scale,
+                    h->mass_in, h->mass_out, h->gram_part, h->mom_part, h->sweeps};
+    for (void* p : ptrs)
+        if (p) (void)hipFree(p);
+}
+
+size_t n_param_growth(const slime_ca_config& c) {
+    return c.growth_per_cell ? (size_t)c.pods * c.G * c.G * c.H : (size_t)c.pods * c.H;
+}
+
+int use_handle(slime_ca* h) {
+    if (!h) return fail(SLIME_EINVAL, "handle is NULL");
+    HIP_TRY(hipSetDevice(h->device));
+    return SLIME_OK;
+}
+
+// S1 for one step: per-batch weights (scaled by the deferred mass scale of x),
+// then the projection GEMM(s).
+int run_project(slime_ca* h, const void* x, const float* x_scale, void* P, void* I, void* V,
+                hipStream_t s) {
+    const slime_ca_config& c = h->cfg;
+    const int C = h->C;
+    WeightPrepArgs w{};
+    w.W = h->W;
+    w.scale = x_scale;
+    w.Wt = h->Wt;
+    w.B = c.B;
+    w.C = C;
+    w.D = c.D;
+    w.per_pod = c.B / c.pods;
+    w.nplanes = 3;
+    w.scaled_planes = c.pvi_chain ? 1u : 7u;
+    HIP_TRY(launch_weight_prep(c.dtype, w, s));
+
+    GemmArgs g{};
+    g.rows_per_batch = c.G * c.G;
+    g.M = c.B * c.G * c.G;
+    g.K = C;
+    g.ncol = C;
+    g.bt_batch_stride = 3LL * C * C;
+    if (!c.pvi_chain) {
+        g.A = x;
+        g.Bt = h->Wt;
+        g.N = 3 * C;
+        g.out[0] = P;
+        g.out[1] = I;
+        g.out[2] = V;
+        g.act[0] = 1;
+        g.act[1] = 2;
+        g.act[2] = 0;
+        HIP_TRY(timed(h, h->gemm_ev, s, [&] { return launch_gemm(c.dtype, g, s); }));
+    } else {
+        const void* ins[3] = {x, P, I};
+        void* outs[3] = {P, I, V};
+        const int acts[3] = {1, 2, 0};
+        g.N = C;
+        for (int p = 0; p < 3; ++p) {
+            g.A = ins[p];
+            g.Bt = static_cast<const char*>(h->Wt) + (size_t)p * C * C * h->elem;
+            g.out[0] = outs[p];
+            g.act[0] = acts[p];
+            HIP_TRY(timed(h, h->gemm_ev, s, [&] { return launch_gemm(c.dtype, g, s); }));
+        }
+    }
+    return SLIME_OK;
+}
+
+// S2-S6 plus the mass partials and S7 finalize: y_raw gets the unscaled output,
+// out_scale the per-(b, head) conservation factor.
+int run_stencil(slime_ca* h, const void* x, const float* x_scale, const void* P, const void* I,
+                const void* V, void* y_raw, float* out_scale, hipStream_t s) {
+    const slime_ca_config& c = h->cfg;
+    StencilArgs a{};
+    a.X = x;
+    a.scale_in = x_scale;
+    a.P = P;
+    a.I = I;
+    a.V = V;
+    a.Y = y_raw;
+    a.K = h->K;
+    a.mu = h->mu;
+    a.sigma = h->sigma;
+    a.M = h->M;
+    a.part_in = h->part_in;
+    a.part_out = h->part_out;
+    a.B = c.B;
+    a.G = c.G;
+    a.D = c.D;
+    a.per_pod = c.B / c.pods;
+    a.per_cell = c.growth_per_cell;
+    a.dt = c.dt;
+    HIP_TRY(timed(h, h->stencil_ev, s, [&] { return launch_stencil(c.dtype, a, s); }));
+    HIP_TRY(launch_mass_finalize(h->part_in, h->part_out, c.B * c.H, h->tiles, h->mass_in,
+                                 h->mass_out, out_scale, s));
+    return SLIME_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* slime_ca_last_error(void) { return g_err.c_str(); }
+
+int slime_ca_create(const slime_ca_config* config, slime_ca** out) {
+    if (!out) return fail(SLIME_EINVAL, "out is NULL");
+    *out = nullptr;
+    int rc = validate(config);
+    if (rc) return rc;
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev < 1)
+        return fail(SLIME_ENODEV, "no HIP device visible");
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev));
+    hipDeviceProp_t prop;
+    HIP_TRY(hipGetDeviceProperties(&prop, dev));
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(SLIME_ENODEV, "device %d is %s; this library is built for gfx950", dev,
+                    prop.gcnArchName);
+
+    slime_ca* h = new slime_ca();
+    h->cfg = *config;
+    h->device = dev;
+    const slime_ca_config& c = h->cfg;
+    h->C = c.H * c.D;
+    h->elem = c.dtype == SLIME_BF16 ? 2 : 4;
+    h->tiles = stencil_tiles_per_batch(c.G);
+    h->state_elems = (long long)c.B * c.G * c.G * h->C;
+    const size_t C = h->C, BH = (size_t)c.B * c.H;
+    const size_t state_bytes = (size_t)h->state_elems * h->elem;
+
+    rc = 0;
+    rc = rc ? rc : dalloc_t(&h->W, (size_t)c.pods * 3 * C * C * 4);
+    rc = rc ? rc : dalloc(&h->Wt, (size_t)c.B * 3 * C * C * h->elem);
+    rc = rc ? rc : dalloc_t(&h->K, (size_t)c.pods * c.H * 9 * 4);
+    rc = rc ? rc : dalloc_t(&h->mu, n_param_growth(c) * 4);
+    rc = rc ? rc : dalloc_t(&h->sigma, n_param_growth(c) * 4);
+    rc = rc ? rc : dalloc_t(&h->M, (size_t)c.pods * c.H * c.H * 4);
+    rc = rc ? rc : dalloc(&h->P, state_bytes);
+    rc = rc ? rc : dalloc(&h->I, state_bytes);
+    rc = rc ? rc : dalloc(&h->V, state_bytes);
+    rc = rc ? rc : dalloc(&h->S[0], state_bytes);
+    rc = rc ? rc : dalloc(&h->S[1], state_bytes);
+    rc = rc ? rc : dalloc_t(&h->part_in, BH * h->tiles * 4);
+    rc = rc ? rc : dalloc_t(&h->part_out, BH * h->tiles * 4);
+    rc = rc ? rc : dalloc_t(&h->scale[0], BH * 4);
+    rc = rc ? rc : dalloc_t(&h->scale[1], BH * 4);
+    rc = rc ? rc : dalloc_t(&h->unit_scale, BH * 4);
+    rc = rc ? rc : dalloc_t(&h->mass_in, BH * 8);
+    rc = rc ? rc : dalloc_t(&h->mass_out, BH * 8);
+    rc = rc ? rc : dalloc_t(&h->sweeps, BH * sizeof(int));
+    if (rc) {
+        release(h);
+        delete h;
+        return rc;
+    }
+    float* ones = new float[BH];
+    for (size_t i = 0; i < BH; ++i) ones[i] = 1.0f;
+    hipError_t e = hipMemcpy(h->unit_scale, ones, BH * 4, hipMemcpyHostToDevice);
+    delete[] ones;
+    if (e == hipSuccess) e = hipMemset(h->mass_in, 0, BH * 8);
+    if (e == hipSuccess) e = hipMemset(h->mass_out, 0, BH * 8);
+    if (e != hipSuccess) {
+        release(h);
+        delete h;
+        return fail(SLIME_EHIP, "initialising handle buffers: %s", hipGetErrorString(e));
+    }
+    *out = h;
+    return SLIME_OK;
+}
+
+int slime_ca_destroy(slime_ca* h) {
+    if (!h) return SLIME_OK;
+    (void)hipSetDevice(h->device);
+    (void)hipDeviceSynchronize();
+    release(h);
+    delete h;
+    return SLIME_OK;
+}
+
+int slime_ca_set_params(slime_ca* h, const slime_ca_params* p) {
+    int rc = use_handle(h);
+    if (rc) return rc;
+    if (!p || !p->WP || !p->WI || !p->WV || !p->K || !p->mu || !p->sigma || !p->M)
+        return fail(SLIME_EINVAL, "a parameter pointer is NULL");
+    const slime_ca_config& c = h->cfg;
+    const size_t C = h->C, CC = C * C;
+    // Masters are kept as [pods][plane][C][C] so plane p of pod q is contiguous.
+    for (int q = 0; q < c.pods; ++q) {
+        const float* src[3] = {p->WP, p->WI, p->WV};
+        for (int pl = 0; pl < 3; ++pl)
+            HIP_TRY(hipMemcpy(h->W + ((size_t)q * 3 + pl) * CC, src[pl] + (size_t)q * CC, CC * 4,
+                              hipMemcpyHostToDevice));
+    }
+    const size_t ng = n_param_growth(c);
+    for (size_t i = 0; i < ng; ++i)
+        if (!std::isfinite(p->sigma[i]) || !std::isfinite(p->mu[i]))
+            return fail(SLIME_EINVAL, "mu/sigma entry %zu is not finite", i);
+    HIP_TRY(hipMemcpy(h->K, p->K, (size_t)c.pods * c.H * 9 * 4, hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy(h->mu, p->mu, ng * 4, hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy(h->sigma, p->sigma, ng * 4, hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy(h->M, p->M, (size_t)c.pods * c.H * c.H * 4, hipMemcpyHostToDevice));
+    h->params_set = true;
+    return SLIME_OK;
+}
+
+int slime_ca_project(slime_ca* h, const void* x_in, void* P, void* I, void* V, void* stream) {
+    int rc = use_handle(h);
+    if (rc) return rc;
+    if (!h->params_set) return fail(SLIME_ESTATE, "slime_ca_set_params has not been called");
+    if (!x_in || !P || !I || !V) return fail(SLIME_EINVAL, "a tensor pointer is NULL");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    h->last_stream = s;
+    return run_project(h, x_in, nullptr, P, I, V, s);
+}
+
+int slime_ca_flow_lenia(slime_ca* h, const void* x_in, const void* P, const void* I, const void* V,
+                        void* y_out, void* stream) {
+    int rc = use_handle(h);
+    if (rc) return rc;
+    if (!h->params_set) return fail(SLIME_ESTATE, "slime_ca_set_params has not been called");
+    if (!x_in || !P || !I || !V || !y_out) return fail(SLIME_EINVAL, "a tensor pointer is NULL");
+    if (y_out == x_in || y_out == P || y_out == I || y_out == V)
+        return fail(SLIME_EINVAL, "y_out aliases an input");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    h->last_stream = s;
+    const slime_ca_config& c = h->cfg;
+    rc = run_stencil(h, x_in, nullptr, P, I, V, h->S[0], h->scale[0], s);
+    if (rc) return rc;
+    HIP_TRY(launch_rescale(c.dtype, h->S[0], h->scale[0], y_out, c.B, c.G, h->C, c.D, s));
+    return SLIME_OK;
+}
+
+int slime_ca_step(slime_ca* h, const void* x_in, void* x_out, int n_steps, void* stream) {
+    int rc = use_handle(h);
+    if (rc) return rc;
+    if (!h->params_set) return fail(SLIME_ESTATE, "slime_ca_set_params has not been called");
+    if (!x_in || !x_out) return fail(SLIME_EINVAL, "a tensor pointer is NULL");
+    if (n_steps < 0) return fail(SLIME_EINVAL, "n_steps=%d is negative", n_steps);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    h->last_stream = s;
+    const slime_ca_config& c = h->cfg;
+    if (n_steps == 0) {
+        if (x_out != x_in)
+            HIP_TRY(hipMemcpyAsync(x_out, x_in, (size_t)h->state_elems * h->elem,
+                                   hipMemcpyDeviceToDevice, s));
+        return SLIME_OK;
+    }
+    const void* cur = x_in;
+    const float* cur_scale = h->unit_scale;
+    for (int i = 0; i < n_steps; ++i) {
+        void* y = h->S[i & 1];
+        float* ys = h->scale[i & 1];
+        rc = run_project(h, cur, cur_scale, h->P, h->I, h->V, s);
+        if (rc) return rc;
+        rc = run_stencil(h, cur, cur_scale, h->P, h->I, h->V, y, ys, s);
+        if (rc) return rc;
+        cur = y;
+        cur_scale = ys;
+    }
+    HIP_TRY(launch_rescale(c.dtype, cur, cur_scale, x_out, c.B, c.G, h->C, c.D, s));
+    return SLIME_OK;
+}
+
+int slime_ca_mass(slime_ca* h, double* h_in, double* h_out) {
+    int rc = use_handle(h);
+    if (rc) return rc;
+    if (!h_in && !h_out) return fail(SLIME_EINVAL, "both outputs are NULL");
+    const size_t BH = (size_t)h->cfg.B * h->cfg.H;
+    HIP_TRY(hipStreamSynchronize(h->last_stream));
+    if (h_in) HIP_TRY(hipMemcpy(h_in, h->mass_in, BH * 8, hipMemcpyDeviceToHost));
+    if (h_out) HIP_TRY(hipMemcpy(h_out, h->mass_out, BH * 8, hipMemcpyDeviceToHost));
+    return SLIME_OK;
+}
+
+int slime_ca_fitness(slime_ca* h, const void* x_hist, int T, float* erank, float* coherence,
+                     float* fitness, void* stream) {
+    int rc = use_handle(h);
+    if (rc) return rc;
+    if (!x_hist || !erank || !coherence || !fitness)
+        return fail(SLIME_EINVAL, "a tensor pointer is NULL");
+    if (T < 2 || T > 65) return fail(SLIME_EINVAL, "T=%d must be in [2, 65]", T);
+    const slime_ca_config& c = h->cfg;
+    const size_t BH = (size_t)c.B * c.H;
+    const int chunks = fitness_chunks(c.G);
+    if (chunks < 1) return fail(SLIME_EINVAL, "grid too small for the fitness pass");
+    if (!h->gram_part || h->fit_chunks != chunks) {
+        if (h->gram_part) (void)hipFree(h->gram_part);
+        h->gram_part = nullptr;
+        rc = dalloc_t(&h->gram_part, BH * chunks * c.D * c.D * 4);
+        if (rc) return rc;
+        h->fit_chunks = chunks;
+    }
+    if (!h->mom_part || h->fit_T < T) {
+        if (h->mom_part) (void)hipFree(h->mom_part);
+        h->mom_part = nullptr;
+        rc = dalloc_t(&h->mom_part, BH * chunks * (size_t)(T - 1) * 5 * 4);
+        if (rc) return rc;
+        h->fit_T = T;
+    }
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    h->last_stream = s;
+    FitnessArgs f{};
+    f.hist = x_hist;
+    f.T = T;
+    f.B = c.B;
+    f.G = c.G;
+    f.D = c.D;
+    f.gram_part = h->gram_part;
+    f.mom_part = h->mom_part;
+    f.chunks = chunks;
+    f.erank = erank;
+    f.coh = coherence;
+    f.fitness = fitness;
+    f.sweeps = h->sweeps;
+    HIP_TRY(launch_fitness(c.dtype, f, s));
+    return SLIME_OK;
+}
+
+int slime_ca_fitness_sweeps(slime_ca* h, int* h_sweeps) {
+    int rc = use_handle(h);
+    if (rc) return rc;
+    if (!h_sweeps) return fail(SLIME_EINVAL, "output is NULL");
+    HIP_TRY(hipStreamSynchronize(h->last_stream));
+    HIP_TRY(hipMemcpy(h_sweeps, h->sweeps, (size_t)h->cfg.B * h->cfg.H * sizeof(int),
+                      hipMemcpyDeviceToHost));
+    return SLIME_OK;
+}
+
+int slime_ca_init_from_field(slime_ca* h, const float* conc, void* x, void* stream) {
+    int rc = use_handle(h);
+    if (rc) return rc;
+    if (!conc || !x) return fail(SLIME_EINVAL, "a tensor pointer is NULL");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    h->last_stream = s;
+    HIP_TRY(launch_init_from_field(h->cfg.dtype, conc, x, h->cfg.G, h->C, s));
+    return SLIME_OK;
+}
+
+int slime_ca_field_from_state(slime_ca* h, const void* x, float* conc, void* stream) {
+    int rc = use_handle(h);
+    if (rc) return rc;
+    if (!conc || !x) return fail(SLIME_EINVAL, "a tensor pointer is NULL");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    h->last_stream = s;
+    HIP_TRY(launch_field_from_state(h->cfg.dtype, x, conc, h->cfg.G, h->C, s));
+    return SLIME_OK;
+}
+
+int slime_ca_set_timing(slime_ca* h, int enable) {
+    int rc = use_handle(h);
+    if (rc) return rc;
+    if (h->last_stream || h->ev_used) HIP_TRY(hipStreamSynchronize(h->last_stream));
+    h->timing = enable != 0;
+    h->ev_used = 0;
+    h->gemm_ev.clear();
+    h->stencil_ev.clear();
+    return SLIME_OK;
+}
+
+int slime_ca_timings(slime_ca* h, double* gemm_ms, int* gemm_n, double* stencil_ms, int* stencil_n) {
+    int rc = use_handle(h);
+    if (rc) return rc;
+    HIP_TRY(hipStreamSynchronize(h->last_stream));
+    auto sum = [&](const std::vector<std::pair<size_t, size_t>>& log, double* ms, int* n) -> int {
+        double tot = 0.0;
+        for (const auto& pr : log) {
+            float t = 0.f;
+            HIP_TRY(hipEventElapsedTime(&t, h->ev_pool[pr.first], h->ev_pool[pr.second]));
+            tot += t;
+        }
+        if (ms) *ms = tot;
+        if (n) *n = (int)log.size();
+        return SLIME_OK;
+    };
+    rc = sum(h->gemm_ev, gemm_ms, gemm_n);
+    if (rc) return rc;
+    return sum(h->stencil_ev, stencil_ms, stencil_n);
+}
+
+int slime_ca_uses_mfma(const slime_ca* h) {
+    if (!h) return 0;
+    const slime_ca_config& c = h->cfg;
+    GemmArgs g{};
+    g.M = c.B * c.G * c.G;
+    g.N = c.pvi_chain ? h->C : 3 * h->C;
+    g.K = h->C;
+    g.ncol = h->C;
+    g.rows_per_batch = c.G * c.G;
+    return gemm_uses_mfma(c.dtype, g) ? 1 : 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,105 @@
+// common.hpp — shared device helpers for the gfx950 CA kernels.
+//
+// Storage types are fp32 or bf16 (raw 16-bit words); every kernel computes in
+// fp32 (Jacobi in fp64). Wavefronts are 64 lanes.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace slime {
+
+typedef uint16_t bf16_t;  // raw bfloat16 bits
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_v;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_v;
+typedef __attribute__((ext_vector_type(16))) float f32x16;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float bf16_to_f32(bf16_t v) {
+    return __builtin_bit_cast(float, (uint32_t)v << 16);
+}
+__device__ __forceinline__ float bf16lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
+__device__ __forceinline__ float bf16hi(uint32_t w) {
+    return __builtin_bit_cast(float, w & 0xffff0000u);
+}
+// Round-to-nearest-even fp32 -> bf16 (NaN stays NaN).
+__device__ __forceinline__ bf16_t f32_to_bf16(float f) {
+    uint32_t u = __builtin_bit_cast(uint32_t, f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)((u >> 16) | 0x40);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (bf16_t)(u >> 16);
+}
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+}
+
+// Storage-type traits: load/store pairs of adjacent channels as float2.
+template <typename T> struct Store;
+template <> struct Store<float> {
+    static constexpr int kBytes = 4;
+    __device__ static __forceinline__ float2 load2(const float* p) {
+        return *reinterpret_cast<const float2*>(p);
+    }
+    __device__ static __forceinline__ void store2(float* p, float a, float b) {
+        *reinterpret_cast<float2*>(p) = make_float2(a, b);
+    }
+    __device__ static __forceinline__ float round(float v) { return v; }
+    __device__ static __forceinline__ float to_f32(float v) { return v; }
+    __device__ static __forceinline__ float from_f32(float v) { return v; }
+};
+template <> struct Store<bf16_t> {
+    static constexpr int kBytes = 2;
+    __device__ static __forceinline__ float2 load2(const bf16_t* p) {
+        const uint32_t w = *reinterpret_cast<const uint32_t*>(p);
+        return make_float2(bf16lo(w), bf16hi(w));
+    }
+    __device__ static __forceinline__ void store2(bf16_t* p, float a, float b) {
+        *reinterpret_cast<uint32_t*>(p) = pack_bf16x2(a, b);
+    }
+    __device__ static __forceinline__ float round(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+    __device__ static __forceinline__ float to_f32(bf16_t v) { return bf16_to_f32(v); }
+    __device__ static __forceinline__ bf16_t from_f32(float v) { return f32_to_bf16(v); }
+};
+
+// ---- wave64 reductions -------------------------------------------------------
+// DPP steps inside each 16-lane row (quad_perm 1,0,3,2; quad_perm 2,3,0,1;
+// row_half_mirror; row_mirror) leave every lane holding its row's sum; the four
+// row sums are then combined through v_readlane, so the result is uniform.
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_f32<0x141>(v);  // row_half_mirror
+    v += dpp_f32<0x140>(v);  // row_mirror
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+    v = row16_sum(v);
+    const int iv = __builtin_bit_cast(int, v);
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 48));
+    return (r0 + r1) + (r2 + r3);
+}
+
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float rcp_fast(float x) { return __builtin_amdgcn_rcpf(x); }
+
+// tanh-GELU written as x * sigmoid(2u), u = sqrt(2/pi) (x + 0.044715 x^3):
+// 0.5 x (1 + tanh u) = x / (1 + exp(-2u)). exp(-2u) = 2^(x (k0 + k1 x^2)).
+__device__ __forceinline__ float gelu_tanh(float x) {
+    constexpr float kLog2e = 1.4426950408889634f;
+    constexpr float k0 = -2.0f * 0.7978845608028654f * kLog2e;
+    constexpr float k1 = k0 * 0.044715f;
+    const float e = exp2_fast(x * __builtin_fmaf(k1, x * x, k0));
+    return x * rcp_fast(1.0f + e);
+}
+
+}  // namespace slime

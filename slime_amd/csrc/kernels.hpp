@@ -1,0 +1,90 @@
+// kernels.hpp — host-side launchers for the gfx950 CA kernels (internal).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace slime {
+
+constexpr int kHeads = 8;  // NUM_HEADS, slime/core/pseudopod.cu:15
+
+// ---- S1 projections ----------------------------------------------------------
+// out_p[m][col] = act_p( sum_k A[m][k] * Bt[batch(m)][n][k] ), n = p*ncol + col.
+struct GemmArgs {
+    const void* A;             // [M][K] rows (cells), K contiguous
+    const void* Bt;            // per batch [N][K], K contiguous
+    long long bt_batch_stride; // elements between consecutive batches' Bt
+    int rows_per_batch;        // rows of A that share one Bt (G*G)
+    int M, N, K;
+    void* out[3];              // output planes [M][ncol]
+    int ncol;                  // columns per plane
+    int act[3];                // 0 identity, 1 ReLU, 2 tanh-GELU
+};
+// Returns true when the MFMA tile kernel handles this shape (else the generic
+// kernel runs). dtype: 0 fp32, 1 bf16.
+bool gemm_uses_mfma(int dtype, const GemmArgs& a);
+hipError_t launch_gemm(int dtype, const GemmArgs& a, hipStream_t s);
+
+// ---- per-batch scaled, transposed weights -------------------------------------
+// Wt[b][p*C + n][k] = cvt( scale_p(b, k) * W[pod(b)][p][k][n] ), where the mass
+// scale applies only to planes that consume the state (scale[b][k / D]).
+struct WeightPrepArgs {
+    const float* W;       // [pods][nplanes][C][C] fp32 masters
+    const float* scale;   // [B][H] or nullptr
+    void* Wt;             // [B][nplanes*C][C]
+    int B, C, D, per_pod, nplanes;
+    unsigned scaled_planes;  // bit p set: plane p is multiplied by the scale
+};
+hipError_t launch_weight_prep(int dtype, const WeightPrepArgs& a, hipStream_t s);
+
+// ---- S2-S6 fused stencil --------------------------------------------------------
+struct StencilArgs {
+    const void* X;           // [B][G][G][C] state (stored, before scale)
+    const float* scale_in;   // [B][H] deferred mass scale for X (nullptr = 1)
+    const void* P;
+    const void* I;
+    const void* V;
+    void* Y;                 // [B][G][G][C] unscaled output
+    const float* K;          // [pods][H][9]
+    const float* mu;         // [pods][H] or [pods][G][G][H]
+    const float* sigma;
+    const float* M;          // [pods][H][H]
+    float* part_in;          // [B][H][tiles]  sum of scaled X per tile
+    float* part_out;         // [B][H][tiles]  sum of stored Y per tile
+    int B, G, D, per_pod, per_cell;
+    float dt;
+};
+int stencil_tiles_per_batch(int G);
+hipError_t launch_stencil(int dtype, const StencilArgs& a, hipStream_t s);
+
+// ---- S7 mass conservation ------------------------------------------------------------
+// scale[b][h] = |sum_out| > 1e-6 ? sum_in / sum_out : 1, reduced in fixed order.
+hipError_t launch_mass_finalize(const float* part_in, const float* part_out, int BH, int tiles,
+                                double* mass_in, double* mass_out, float* scale_out,
+                                hipStream_t s);
+// y[i] = cvt(scale[b][h] * x[i]) over the whole state.
+hipError_t launch_rescale(int dtype, const void* x, const float* scale, void* y, int B, int G,
+                          int C, int D, hipStream_t s);
+
+// ---- E1-E5 fitness --------------------------------------------------------------------
+struct FitnessArgs {
+    const void* hist;   // [T][B][G][G][C]
+    int T, B, G, D;
+    float* gram_part;   // [B*H][chunks][D*D]
+    float* mom_part;    // [B*H][chunks][(T-1)*5]
+    int chunks;
+    float* erank;       // [B][H]
+    float* coh;
+    float* fitness;
+    int* sweeps;        // [B][H] Jacobi sweeps used (may be nullptr)
+};
+int fitness_chunks(int G);
+hipError_t launch_fitness(int dtype, const FitnessArgs& a, hipStream_t s);
+
+// ---- organism adapters (slime/core/organism.cu:691-743) -----------------------------
+hipError_t launch_init_from_field(int dtype, const float* conc, void* X, int G, int C,
+                                  hipStream_t s);
+hipError_t launch_field_from_state(int dtype, const void* X, float* conc, int G, int C,
+                                   hipStream_t s);
+
+}  // namespace slime

@@ -1,0 +1,70 @@
+"""CPU checks of the C ABI: the library loads, exports exactly what
+include/slime_ca.h declares, and rejects bad arguments with status codes before
+touching a device (no compute calls: this container has no GPU)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from slime_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _header_functions():
+    with open(os.path.join(ROOT, "include", "slime_ca.h")) as f:
+        text = f.read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(slime_ca_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_exported_set():
+    assert _header_functions() == sorted(_lib.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in _header_functions():
+        assert hasattr(lib, name), name
+
+
+def _cfg(**kw):
+    base = dict(B=1, G=32, H=8, D=8, dtype=_lib.SLIME_F32, dt=0.1, growth_per_cell=0, pods=1,
+                pvi_chain=0)
+    base.update(kw)
+    return _lib.Config(**base)
+
+
+@pytest.mark.parametrize("bad", [dict(B=0), dict(G=12), dict(G=4), dict(H=4), dict(D=48),
+                                 dict(dtype=7), dict(pods=3), dict(dt=float("nan")),
+                                 dict(growth_per_cell=2), dict(pvi_chain=5)])
+def test_create_rejects_invalid_config(bad):
+    lib = _lib.load()
+    h = ctypes.c_void_p()
+    rc = lib.slime_ca_create(ctypes.byref(_cfg(**bad)), ctypes.byref(h))
+    assert rc == _lib.SLIME_EINVAL
+    assert not h.value
+    assert lib.slime_ca_last_error()
+
+
+def test_null_arguments_are_errors_not_crashes():
+    lib = _lib.load()
+    assert lib.slime_ca_create(None, None) == _lib.SLIME_EINVAL
+    h = ctypes.c_void_p()
+    assert lib.slime_ca_create(None, ctypes.byref(h)) == _lib.SLIME_EINVAL
+    assert lib.slime_ca_step(None, None, None, 1, None) == _lib.SLIME_EINVAL
+    assert lib.slime_ca_set_params(None, None) == _lib.SLIME_EINVAL
+    assert lib.slime_ca_destroy(None) == _lib.SLIME_OK
+    assert lib.slime_ca_uses_mfma(None) == 0
+    assert b"NULL" in lib.slime_ca_last_error()
+
+
+def test_valid_config_without_gpu_reports_no_device():
+    if os.path.exists("/dev/kfd"):
+        pytest.skip("a GPU is visible; covered by the gpu tests")
+    lib = _lib.load()
+    h = ctypes.c_void_p()
+    rc = lib.slime_ca_create(ctypes.byref(_cfg()), ctypes.byref(h))
+    assert rc in (_lib.SLIME_ENODEV, _lib.SLIME_EHIP)
+    assert not h.value

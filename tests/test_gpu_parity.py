@@ -1,0 +1,300 @@
+"""GPU parity: the HIP library (through its C ABI) against the CPU oracle on the
+same seeded inputs.
+
+Tolerances (the parity metric is max|gpu - ref| / max|ref| per tensor):
+  fp32 state and weights: 1e-5;  bf16 state and weights: 2e-2.
+  Mass: |sum_out - sum_in| <= 1e-6 |sum_in| per (batch, head), asserted on the
+  conserved fp32 result (for bf16 on the value before the final rounding, with
+  the rounding drift of the stored tensor bounded separately).
+"""
+import numpy as np
+import pytest
+
+from slime_amd import Pseudopod, make_params, make_state, round_bf16
+from slime_amd.synthetic import CAConfig
+from tests.conftest import norm_err
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+TOL = {"fp32": 1e-5, "bf16": 2e-2}
+
+
+@pytest.fixture(autouse=True)
+def _needs_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+
+
+def _ocfg(cfg, **kw):
+    from oracle import OracleConfig
+    base = dict(B=cfg.B, G=cfg.G, H=cfg.H, D=cfg.D, pods=cfg.pods,
+                growth_per_cell=cfg.growth_per_cell, dt=cfg.dt)
+    base.update(kw)
+    return OracleConfig(**base)
+
+
+def _prep(cfg, pseed=1, sseed=2):
+    """Params and state as the device sees them (bf16-rounded when bf16)."""
+    p = make_params(cfg, seed=pseed)
+    X = make_state(cfg, seed=sseed)
+    if cfg.dtype == "bf16":
+        p = {k: (round_bf16(v) if k in ("WP", "WI", "WV") else v) for k, v in p.items()}
+        X = round_bf16(X)
+    return p, X
+
+
+def _dev(a, dtype):
+    t = torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).cuda()
+    return t.to(torch.bfloat16 if dtype == "bf16" else torch.float32).contiguous()
+
+
+def _host(t):
+    return t.float().cpu().numpy()
+
+
+def _engine(cfg, pvi_chain=False, **kw):
+    print(f"[case] {cfg.name} B={cfg.B} G={cfg.G} D={cfg.D} {cfg.dtype} pods={cfg.pods} "
+          f"per_cell={cfg.growth_per_cell} chain={pvi_chain}", flush=True)
+    e = Pseudopod(cfg.B, cfg.G, cfg.H, cfg.D, cfg.dtype, cfg.dt, cfg.growth_per_cell, cfg.pods,
+                  pvi_chain, **kw)
+    return e
+
+
+def _cfg(name, B, G, D, dtype, **kw):
+    return CAConfig(name, B=B, G=G, H=8, D=D, dtype=dtype, steps=1, w_std=0.05, **kw)
+
+
+def _oracle_flow(oracle, ocfg, X, P, I, V, p):
+    U = oracle.potential(ocfg, X, p["K"])
+    g = oracle.growth(ocfg, U, p["mu"], p["sigma"])
+    A = oracle.attention(ocfg, P, I)
+    Vt = oracle.propagate(ocfg, A, V)
+    Y = oracle.mix(ocfg, X, g, Vt, p["M"])
+    return oracle.conserve(ocfg, X, Y)
+
+
+# ---- configuration c1 against the committed golden fixture and the oracle ----------------
+
+def test_c1_step_matches_golden_and_oracle(oracle):
+    from slime_amd import CONFIGS
+    from tests.golden.make_golden import check_c1
+    cfg = CONFIGS["c1"]
+    p, X = _prep(cfg)
+    with _engine(cfg) as e:
+        e.set_params(p)
+        y = e.forward(_dev(X, cfg.dtype))
+        torch.cuda.synchronize()
+        mi, mo = e.mass()
+        Y = _host(y)
+    check_c1(Y, tol=TOL["fp32"])
+    ref, rmi, _ = oracle.step(_ocfg(cfg), X, p, 1)
+    assert norm_err(Y, ref) <= TOL["fp32"]
+    np.testing.assert_allclose(mi, rmi, rtol=1e-6)
+    np.testing.assert_allclose(mo, mi, rtol=1e-6)
+    ys = Y.astype(np.float64).reshape(cfg.B, -1, cfg.H, cfg.D).sum(axis=(1, 3))
+    np.testing.assert_allclose(ys, rmi, rtol=1e-6)
+
+
+# ---- stage by stage, MFMA projection path ----------------------------------------------------
+
+@pytest.mark.parametrize("dtype", ["fp32", "bf16"])
+def test_project_mfma_matches_oracle(oracle, dtype):
+    cfg = _cfg("proj", B=2, G=16, D=64, dtype=dtype)
+    p, X = _prep(cfg)
+    with _engine(cfg) as e:
+        assert e.uses_mfma
+        e.set_params(p)
+        P, I, V = e.project(_dev(X, dtype))
+        torch.cuda.synchronize()
+        got = [_host(t) for t in (P, I, V)]
+    ref = oracle.project(_ocfg(cfg), X, p["WP"], p["WI"], p["WV"])
+    for name, g, r in zip("PIV", got, ref):
+        err = norm_err(g, r)
+        print(f"  {name}: normalised error {err:.3e}")
+        assert err <= TOL[dtype], name
+
+
+@pytest.mark.parametrize("dtype", ["fp32", "bf16"])
+def test_flow_lenia_matches_oracle_on_same_projections(oracle, dtype):
+    cfg = _cfg("flow", B=2, G=16, D=64, dtype=dtype)
+    p, X = _prep(cfg)
+    with _engine(cfg) as e:
+        e.set_params(p)
+        x = _dev(X, dtype)
+        P, I, V = e.project(x)
+        y = e.flow_lenia(x, P, I, V)
+        torch.cuda.synchronize()
+        mi, mo = e.mass()
+        hp, hi, hv, Y = (_host(t) for t in (P, I, V, y))
+    ref, rmi, rmo = _oracle_flow(oracle, _ocfg(cfg), X, hp, hi, hv, p)
+    err = norm_err(Y, ref)
+    print(f"  Y: normalised error {err:.3e}")
+    assert err <= TOL[dtype]
+    np.testing.assert_allclose(mi, rmi, rtol=1e-6)
+    np.testing.assert_allclose(mo, mi, rtol=1e-6)
+    drift = np.abs(Y.astype(np.float64).reshape(cfg.B, -1, cfg.H, cfg.D).sum(axis=(1, 3)) - rmi)
+    bound = 1e-6 if dtype == "fp32" else 2e-4  # bf16 store: half-ulp noise summed over 16 K values
+    assert np.all(drift <= bound * np.abs(rmi)), drift / np.abs(rmi)
+
+
+# ---- full steps ------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype,per_cell,pods,chain,D", [
+    ("fp32", False, 1, False, 64),
+    ("fp32", True, 1, False, 64),
+    ("bf16", False, 1, False, 64),
+    ("bf16", False, 2, False, 64),
+    ("fp32", False, 1, True, 32),
+    ("bf16", True, 2, False, 16),
+])
+def test_step_matches_oracle(oracle, dtype, per_cell, pods, chain, D):
+    cfg = _cfg("step", B=2, G=16, D=D, dtype=dtype, growth_per_cell=per_cell, pods=pods)
+    p, X = _prep(cfg)
+    with _engine(cfg, pvi_chain=chain) as e:
+        e.set_params(p)
+        y = e.forward(_dev(X, dtype))
+        torch.cuda.synchronize()
+        mi, mo = e.mass()
+        Y = _host(y)
+    ref, rmi, _ = oracle.step(_ocfg(cfg, pvi_chain=chain), X, p, 1)
+    err = norm_err(Y, ref)
+    print(f"  Y: normalised error {err:.3e}")
+    assert err <= TOL[dtype]
+    np.testing.assert_allclose(mi, rmi, rtol=1e-6)
+    np.testing.assert_allclose(mo, mi, rtol=1e-6)
+
+
+def test_multi_step_fp32_matches_oracle(oracle):
+    cfg = _cfg("multi", B=1, G=16, D=64, dtype="fp32", growth_per_cell=True)
+    p, X = _prep(cfg)
+    with _engine(cfg) as e:
+        e.set_params(p)
+        x = _dev(X, "fp32")
+        y3 = e.forward(x, n_steps=3)
+        torch.cuda.synchronize()
+        mi, mo = e.mass()
+        Y = _host(y3)
+    ref, rmi, _ = oracle.step(_ocfg(cfg), X, p, 3)
+    err = norm_err(Y, ref)
+    print(f"  Y after 3 steps: normalised error {err:.3e}")
+    assert err <= TOL["fp32"]
+    np.testing.assert_allclose(mi, rmi, rtol=1e-6)
+    np.testing.assert_allclose(mo, mi, rtol=1e-6)
+
+
+def test_in_place_and_zero_steps():
+    cfg = _cfg("inplace", B=1, G=16, D=16, dtype="bf16")
+    p, X = _prep(cfg)
+    with _engine(cfg) as e:
+        e.set_params(p)
+        x = _dev(X, "bf16")
+        y_ref = e.forward(x.clone(), n_steps=2)
+        x2 = x.clone()
+        e.forward(x2, out=x2, n_steps=2)
+        x0 = e.forward(x, n_steps=0)
+        torch.cuda.synchronize()
+        assert torch.equal(x2, y_ref)
+        assert torch.equal(x0, x)
+
+
+def test_step_is_deterministic():
+    cfg = _cfg("det", B=2, G=16, D=64, dtype="bf16")
+    p, X = _prep(cfg)
+    with _engine(cfg) as e:
+        e.set_params(p)
+        x = _dev(X, "bf16")
+        a = e.forward(x, n_steps=2)
+        b = e.forward(x, n_steps=2)
+        torch.cuda.synchronize()
+        assert torch.equal(a, b)
+
+
+def test_errors_surface_as_exceptions():
+    from slime_amd import SlimeError
+    cfg = _cfg("err", B=1, G=16, D=8, dtype="fp32")
+    with _engine(cfg) as e:
+        with pytest.raises(SlimeError):
+            e.forward(_dev(make_state(cfg), "fp32"))  # parameters not set yet
+        p, X = _prep(cfg)
+        e.set_params(p)
+        x = _dev(X, "fp32")
+        with pytest.raises(SlimeError):
+            e.flow_lenia(x, x, x, x, out=x)  # output aliases an input
+
+
+# ---- fitness -----------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype,D", [("bf16", 64), ("fp32", 8)])
+def test_fitness_matches_oracle(oracle, dtype, D):
+    cfg = _cfg("fit", B=2, G=16, D=D, dtype=dtype)
+    p, X = _prep(cfg)
+    T = 4
+    with _engine(cfg) as e:
+        e.set_params(p)
+        hist = torch.empty((T,) + e.state_shape, dtype=e.torch_dtype, device="cuda")
+        hist[0] = _dev(X, dtype)
+        for t in range(1, T):
+            e.forward(hist[t - 1], out=hist[t])
+        er, coh, fit = e.fitness(hist)
+        torch.cuda.synchronize()
+        sweeps = e.jacobi_sweeps()
+        H_ = _host(hist)
+        er, coh, fit = _host(er), _host(coh), _host(fit)
+    rer, rcoh, rfit = oracle.fitness(_ocfg(cfg), H_)
+    print(f"  erank max abs diff {np.max(np.abs(er - rer)):.3e}, coh {np.max(np.abs(coh - rcoh)):.3e}")
+    assert np.all(sweeps <= 30)
+    np.testing.assert_allclose(er, rer, atol=0.01)        # buildplan.md:289 criterion
+    np.testing.assert_allclose(coh, rcoh, atol=1e-4)
+    np.testing.assert_allclose(fit, rfit, rtol=1e-3, atol=0.01)
+
+
+def test_fitness_closed_forms():
+    cfg = _cfg("fitcf", B=1, G=16, D=64, dtype="fp32")
+    X = make_state(cfg, seed=5)
+    with _engine(cfg) as e:
+        hist = torch.from_numpy(np.stack([X, X, X])).cuda().contiguous()
+        er, coh, fit = e.fitness(hist)
+        np.testing.assert_allclose(_host(coh), 1.0, atol=1e-5)
+        hist2 = torch.from_numpy(np.stack([X - 0.5, 0.5 - X])).cuda().contiguous()
+        _, coh2, _ = e.fitness(hist2)
+        np.testing.assert_allclose(_host(coh2), 0.0, atol=1e-5)
+
+
+# ---- organism adapters ----------------------------------------------------------------------------
+
+def test_field_adapters_match_oracle(oracle):
+    cfg = _cfg("field", B=1, G=32, D=64, dtype="fp32")
+    conc = np.random.default_rng(3).random((32, 32), dtype=np.float32)
+    with _engine(cfg) as e:
+        x = e.init_from_field(torch.from_numpy(conc))
+        c2 = e.field_from_state(x)
+        torch.cuda.synchronize()
+        X, C2 = _host(x), _host(c2)
+    ref = oracle.init_from_field(conc, cfg.C)
+    assert norm_err(X, ref) <= 1e-6
+    assert norm_err(C2, oracle.field_from_state(ref)) <= 1e-6
+
+
+# ---- full-size throughput shape: size-independent properties --------------------------------------
+
+def test_c3_shape_conserves_mass_and_matches_oracle_on_one_batch(oracle):
+    from slime_amd import CONFIGS
+    cfg = CONFIGS["c3"]
+    p, X = _prep(cfg)
+    with _engine(cfg) as e:
+        e.set_params(p)
+        x = _dev(X, "bf16")
+        y = e.forward(x)
+        torch.cuda.synchronize()
+        mi, mo = e.mass()
+        assert bool(torch.isfinite(y.float()).all())
+        Y0 = _host(y[0:1])
+    np.testing.assert_allclose(mo, mi, rtol=1e-6)
+    one = _ocfg(cfg, B=1)
+    ref, rmi, _ = oracle.step(one, X[0:1], p, 1)
+    err = norm_err(Y0, ref)
+    print(f"  batch 0 of c3: normalised error {err:.3e}")
+    assert err <= TOL["bf16"]
+    np.testing.assert_allclose(mi[0], rmi[0], rtol=1e-6)
