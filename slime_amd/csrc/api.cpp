@@ -40,6 +40,7 @@ struct slime_ca {
     void* I = nullptr;
     void* V = nullptr;
     void* S[2] = {nullptr, nullptr};  // unscaled step outputs (ping-pong)
+    float* Sf = nullptr;       // unscaled fp32 output of a call's last step (bf16 state only)
     float* part_in = nullptr;  // [B*H][tiles]
     float* part_out = nullptr;
     float* scale[2] = {nullptr, nullptr};  // [B*H]
@@ -149,7 +150,7 @@ hipError_t timed(slime_ca* h, std::vector<std::pair<size_t, size_t>>& log, hipSt
 void release(slime_ca* h) {
     for (hipEvent_t e : h->ev_pool) (void)hipEventDestroy(e);
     h->ev_pool.clear();
-    void* ptrs[] = {h->W, h->Wt, h->K, h->mu, h->sigma, h->M, h->P, h->I, h->V, h->S[0], h->S[1],
+    void* ptrs[] = {h->W, h->Wt, h->K, h->mu, h->sigma, h->M, h->P, h->I, h->V, h->S[0], h->S[1], h->Sf,
                     h->part_in, h->part_out, h->scale[0], h->scale[1], h->unit_scale,
                     h->mass_in, h->mass_out, h->gram_part, h->mom_part, h->sweeps};
     for (void* p : ptrs)
@@ -220,7 +221,7 @@ int run_project(slime_ca* h, const void* x, const float* x_scale, void* P, void*
 // S2-S6 plus the mass partials and S7 finalize: y_raw gets the unscaled output,
 // out_scale the per-(b, head) conservation factor.
 int run_stencil(slime_ca* h, const void* x, const float* x_scale, const void* P, const void* I,
-                const void* V, void* y_raw, float* out_scale, hipStream_t s) {
+                const void* V, void* y_raw, int y_f32, float* out_scale, hipStream_t s) {
     const slime_ca_config& c = h->cfg;
     StencilArgs a{};
     a.X = x;
@@ -229,6 +230,7 @@ int run_stencil(slime_ca* h, const void* x, const float* x_scale, const void* P,
     a.I = I;
     a.V = V;
     a.Y = y_raw;
+    a.y_f32 = y_f32;
     a.K = h->K;
     a.mu = h->mu;
     a.sigma = h->sigma;
@@ -292,6 +294,7 @@ int slime_ca_create(const slime_ca_config* config, slime_ca** out) {
     rc = rc ? rc : dalloc(&h->V, state_bytes);
     rc = rc ? rc : dalloc(&h->S[0], state_bytes);
     rc = rc ? rc : dalloc(&h->S[1], state_bytes);
+    if (c.dtype == SLIME_BF16) rc = rc ? rc : dalloc_t(&h->Sf, (size_t)h->state_elems * 4);
     rc = rc ? rc : dalloc_t(&h->part_in, BH * h->tiles * 4);
     rc = rc ? rc : dalloc_t(&h->part_out, BH * h->tiles * 4);
     rc = rc ? rc : dalloc_t(&h->scale[0], BH * 4);
@@ -376,9 +379,12 @@ int slime_ca_flow_lenia(slime_ca* h, const void* x_in, const void* P, const void
     hipStream_t s = static_cast<hipStream_t>(stream);
     h->last_stream = s;
     const slime_ca_config& c = h->cfg;
-    rc = run_stencil(h, x_in, nullptr, P, I, V, h->S[0], h->scale[0], s);
+    // The output is rescaled once from an fp32 copy, so a bf16 state is rounded once.
+    void* raw = h->Sf ? static_cast<void*>(h->Sf) : h->S[0];
+    rc = run_stencil(h, x_in, nullptr, P, I, V, raw, h->Sf != nullptr, h->scale[0], s);
     if (rc) return rc;
-    HIP_TRY(launch_rescale(c.dtype, h->S[0], h->scale[0], y_out, c.B, c.G, h->C, c.D, s));
+    HIP_TRY(launch_rescale(c.dtype, raw, h->Sf != nullptr, h->scale[0], y_out, c.B, c.G, h->C,
+                           c.D, s));
     return SLIME_OK;
 }
 
@@ -399,17 +405,24 @@ int slime_ca_step(slime_ca* h, const void* x_in, void* x_out, int n_steps, void*
     }
     const void* cur = x_in;
     const float* cur_scale = h->unit_scale;
+    // Intermediate outputs stay unscaled in the storage type: the next step applies
+    // the conservation factor in fp32 as it reads them. The last step writes fp32
+    // (bf16 state) so the final rescale rounds once.
+    int cur_f32 = 0;
     for (int i = 0; i < n_steps; ++i) {
-        void* y = h->S[i & 1];
+        const bool last = i == n_steps - 1;
+        const int y_f32 = last && h->Sf != nullptr;
+        void* y = y_f32 ? static_cast<void*>(h->Sf) : h->S[i & 1];
         float* ys = h->scale[i & 1];
         rc = run_project(h, cur, cur_scale, h->P, h->I, h->V, s);
         if (rc) return rc;
-        rc = run_stencil(h, cur, cur_scale, h->P, h->I, h->V, y, ys, s);
+        rc = run_stencil(h, cur, cur_scale, h->P, h->I, h->V, y, y_f32, ys, s);
         if (rc) return rc;
         cur = y;
+        cur_f32 = y_f32;
         cur_scale = ys;
     }
-    HIP_TRY(launch_rescale(c.dtype, cur, cur_scale, x_out, c.B, c.G, h->C, c.D, s));
+    HIP_TRY(launch_rescale(c.dtype, cur, cur_f32, cur_scale, x_out, c.B, c.G, h->C, c.D, s));
     return SLIME_OK;
 }
 

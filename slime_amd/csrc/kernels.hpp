@@ -44,7 +44,8 @@ struct StencilArgs {
     const void* P;
     const void* I;
     const void* V;
-    void* Y;                 // [B][G][G][C] unscaled output
+    void* Y;                 // [B][G][G][C] unscaled output (storage type, or fp32)
+    int y_f32;               // 1: Y is fp32 regardless of the state's storage type
     const float* K;          // [pods][H][9]
     const float* mu;         // [pods][H] or [pods][G][G][H]
     const float* sigma;
@@ -62,9 +63,10 @@ hipError_t launch_stencil(int dtype, const StencilArgs& a, hipStream_t s);
 hipError_t launch_mass_finalize(const float* part_in, const float* part_out, int BH, int tiles,
                                 double* mass_in, double* mass_out, float* scale_out,
                                 hipStream_t s);
-// y[i] = cvt(scale[b][h] * x[i]) over the whole state.
-hipError_t launch_rescale(int dtype, const void* x, const float* scale, void* y, int B, int G,
-                          int C, int D, hipStream_t s);
+// y[i] = cvt(scale[b][h] * x[i]) over the whole state; x is fp32 when x_f32 is
+// set, else in the storage type.
+hipError_t launch_rescale(int dtype, const void* x, int x_f32, const float* scale, void* y, int B,
+                          int G, int C, int D, hipStream_t s);
 
 // ---- E1-E5 fitness --------------------------------------------------------------------
 struct FitnessArgs {

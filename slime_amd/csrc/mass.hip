@@ -47,35 +47,32 @@ __global__ __launch_bounds__(64) void mass_finalize_kernel(const float* part_in,
     }
 }
 
-template <typename T>
-__global__ __launch_bounds__(256) void rescale_kernel(const T* x, const float* scale, T* y,
-                                                      long long nchunks, int C, int D,
+template <typename TI, typename T>
+__global__ __launch_bounds__(256) void rescale_kernel(const TI* x, const float* scale, T* y,
+                                                      long long nquads, int C, int D,
                                                       long long cells_per_batch) {
-    // One 16-byte chunk per thread; a chunk never straddles two heads (D >= chunk).
-    constexpr int kCE = 16 / (int)sizeof(T);
+    // Four consecutive elements per thread; they never straddle two heads (D >= 8).
     const long long q = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (q >= nchunks) return;
-    const long long e0 = q * kCE;
+    if (q >= nquads) return;
+    const long long e0 = q * 4;
     const long long cell = e0 / C;
     const int ch = (int)(e0 - cell * C);
     const int b = (int)(cell / cells_per_batch);
     const float s = scale[b * (C / D) + ch / D];
-    const uint4 v = reinterpret_cast<const uint4*>(x)[q];
-    uint4 o;
-    if constexpr (sizeof(T) == 2) {
-        o.x = pack_bf16x2(bf16lo(v.x) * s, bf16hi(v.x) * s);
-        o.y = pack_bf16x2(bf16lo(v.y) * s, bf16hi(v.y) * s);
-        o.z = pack_bf16x2(bf16lo(v.z) * s, bf16hi(v.z) * s);
-        o.w = pack_bf16x2(bf16lo(v.w) * s, bf16hi(v.w) * s);
+    float v[4];
+    if constexpr (sizeof(TI) == 2) {
+        const uint2 w = reinterpret_cast<const uint2*>(x)[q];
+        v[0] = bf16lo(w.x); v[1] = bf16hi(w.x); v[2] = bf16lo(w.y); v[3] = bf16hi(w.y);
     } else {
-        float4 f = __builtin_bit_cast(float4, v);
-        f.x *= s;
-        f.y *= s;
-        f.z *= s;
-        f.w *= s;
-        o = __builtin_bit_cast(uint4, f);
+        const float4 f = reinterpret_cast<const float4*>(x)[q];
+        v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
     }
-    reinterpret_cast<uint4*>(y)[q] = o;
+    if constexpr (sizeof(T) == 2) {
+        reinterpret_cast<uint2*>(y)[q] =
+            make_uint2(pack_bf16x2(v[0] * s, v[1] * s), pack_bf16x2(v[2] * s, v[3] * s));
+    } else {
+        reinterpret_cast<float4*>(y)[q] = make_float4(v[0] * s, v[1] * s, v[2] * s, v[3] * s);
+    }
 }
 
 }  // namespace
@@ -88,19 +85,23 @@ hipError_t launch_mass_finalize(const float* part_in, const float* part_out, int
     return hipGetLastError();
 }
 
-hipError_t launch_rescale(int dtype, const void* x, const float* scale, void* y, int B, int G,
-                          int C, int D, hipStream_t s) {
+hipError_t launch_rescale(int dtype, const void* x, int x_f32, const float* scale, void* y, int B,
+                          int G, int C, int D, hipStream_t s) {
     const long long cells = (long long)G * G;
-    const long long elems = (long long)B * cells * C;
-    const long long nchunks = elems / (dtype == 1 ? 8 : 4);
-    const dim3 grid((unsigned)((nchunks + 255) / 256));
-    if (dtype == 1)
-        hipLaunchKernelGGL(rescale_kernel<bf16_t>, grid, dim3(256), 0, s,
-                           static_cast<const bf16_t*>(x), scale, static_cast<bf16_t*>(y), nchunks, C,
+    const long long nquads = (long long)B * cells * C / 4;
+    const dim3 grid((unsigned)((nquads + 255) / 256));
+    if (dtype == 1 && x_f32)
+        hipLaunchKernelGGL((rescale_kernel<float, bf16_t>), grid, dim3(256), 0, s,
+                           static_cast<const float*>(x), scale, static_cast<bf16_t*>(y), nquads, C,
+                           D, cells);
+    else if (dtype == 1)
+        hipLaunchKernelGGL((rescale_kernel<bf16_t, bf16_t>), grid, dim3(256), 0, s,
+                           static_cast<const bf16_t*>(x), scale, static_cast<bf16_t*>(y), nquads, C,
                            D, cells);
     else
-        hipLaunchKernelGGL(rescale_kernel<float>, grid, dim3(256), 0, s, static_cast<const float*>(x),
-                           scale, static_cast<float*>(y), nchunks, C, D, cells);
+        hipLaunchKernelGGL((rescale_kernel<float, float>), grid, dim3(256), 0, s,
+                           static_cast<const float*>(x), scale, static_cast<float*>(y), nquads, C,
+                           D, cells);
     return hipGetLastError();
 }
 

@@ -105,7 +105,9 @@ __device__ __forceinline__ void chunk_to_f32(float* dst, uint4 v, float s) {
     }
 }
 
-template <typename T, int D>
+// TY: storage type of the unscaled output; fp32 when the caller rescales it into
+// the final bf16 state (one rounding instead of two).
+template <typename T, int D, typename TY>
 __global__ __launch_bounds__((Layout<T, D>::kThreads), 2) void stencil_kernel(StencilArgs a) {
     using L = Layout<T, D>;
     constexpr int H = kHeads;
@@ -310,7 +312,7 @@ __global__ __launch_bounds__((Layout<T, D>::kThreads), 2) void stencil_kernel(St
     }
 
     // ---- phase C: store Y (storage type) and the tile's mass partial sums ---------
-    T* Yg = static_cast<T*>(a.Y);
+    TY* Yg = static_cast<TY*>(a.Y);
     float ysum[H];
 #pragma unroll
     for (int o = 0; o < H; ++o) ysum[o] = 0.f;
@@ -320,10 +322,10 @@ __global__ __launch_bounds__((Layout<T, D>::kThreads), 2) void stencil_kernel(St
             const long long base = (batch_base + (long long)(ty0 + ry) * G + tx0 + rx0 + x) * C + c0;
 #pragma unroll
             for (int o = 0; o < H; ++o) {
-                const float r0 = Store<T>::round(y[o][x][0]);
-                const float r1 = Store<T>::round(y[o][x][1]);
+                const float r0 = Store<TY>::round(y[o][x][0]);
+                const float r1 = Store<TY>::round(y[o][x][1]);
                 ysum[o] += r0 + r1;
-                Store<T>::store2(Yg + base + o * D, r0, r1);
+                Store<TY>::store2(Yg + base + o * D, r0, r1);
             }
         }
     }
@@ -347,19 +349,25 @@ __global__ __launch_bounds__((Layout<T, D>::kThreads), 2) void stencil_kernel(St
     }
 }
 
-template <typename T, int D>
-hipError_t launch_td(const StencilArgs& a, hipStream_t s) {
+template <typename T, int D, typename TY>
+hipError_t launch_tdy(const StencilArgs& a, hipStream_t s) {
     using L = Layout<T, D>;
     static bool attr_set = false;
     if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void*)stencil_kernel<T, D>,
+        hipError_t e = hipFuncSetAttribute((const void*)stencil_kernel<T, D, TY>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, L::kBytes);
         if (e != hipSuccess) return e;
         attr_set = true;
     }
     const int tiles = (a.G / kTileY) * (a.G / kTileX);
-    hipLaunchKernelGGL((stencil_kernel<T, D>), dim3(a.B * tiles), dim3(L::kThreads), L::kBytes, s, a);
+    hipLaunchKernelGGL((stencil_kernel<T, D, TY>), dim3(a.B * tiles), dim3(L::kThreads), L::kBytes,
+                       s, a);
     return hipGetLastError();
+}
+
+template <typename T, int D>
+hipError_t launch_td(const StencilArgs& a, hipStream_t s) {
+    return a.y_f32 ? launch_tdy<T, D, float>(a, s) : launch_tdy<T, D, T>(a, s);
 }
 
 template <typename T>

@@ -135,7 +135,10 @@ def test_flow_lenia_matches_oracle_on_same_projections(oracle, dtype):
     np.testing.assert_allclose(mi, rmi, rtol=1e-6)
     np.testing.assert_allclose(mo, mi, rtol=1e-6)
     drift = np.abs(Y.astype(np.float64).reshape(cfg.B, -1, cfg.H, cfg.D).sum(axis=(1, 3)) - rmi)
-    bound = 1e-6 if dtype == "fp32" else 2e-4  # bf16 store: half-ulp noise summed over 16 K values
+    # bf16: one rounding of each stored element; the sum over 16 K elements of
+    # ~U[0,1) values carries ~1e-5 relative noise (4 sigma ~ 4e-5). A second,
+    # biased rounding (rescaling already-rounded values) would show up as ~1e-4.
+    bound = 1e-6 if dtype == "fp32" else 5e-5
     assert np.all(drift <= bound * np.abs(rmi)), drift / np.abs(rmi)
 
 
@@ -274,7 +277,10 @@ def test_field_adapters_match_oracle(oracle):
         X, C2 = _host(x), _host(c2)
     ref = oracle.init_from_field(conc, cfg.C)
     assert norm_err(X, ref) <= 1e-6
-    assert norm_err(C2, oracle.field_from_state(ref)) <= 1e-6
+    # The channel mean of conc*sin(0.1c) cancels heavily (|mean| << mean |X|): bound
+    # the error by fp32 summation noise relative to the magnitudes summed.
+    scale = np.abs(ref).mean(axis=-1)
+    assert np.max(np.abs(C2 - oracle.field_from_state(ref)) / scale) <= 1e-6
 
 
 # ---- full-size throughput shape: size-independent properties --------------------------------------
