@@ -30,7 +30,7 @@ struct slime_ca {
     bool params_set = false;
     hipStream_t last_stream = nullptr;
 
-    float* W = nullptr;        // [pods][3][C][C] fp32 masters
+    float* Wtm = nullptr;      // [pods][3C][C] fp32 masters, transposed (n-major)
     void* Wt = nullptr;        // [B][3C][C] per-batch scaled, transposed
     float* K = nullptr;        // [pods][H][9]
     float* mu = nullptr;       // [pods][H] or [pods][G][G][H]
@@ -150,7 +150,7 @@ hipError_t timed(slime_ca* h, std::vector<std::pair<size_t, size_t>>& log, hipSt
 void release(slime_ca* h) {
     for (hipEvent_t e : h->ev_pool) (void)hipEventDestroy(e);
     h->ev_pool.clear();
-    void* ptrs[] = {h->W, h->Wt, h->K, h->mu, h->sigma, h->M, h->P, h->I, h->V, h->S[0], h->S[1], h->Sf,
+    void* ptrs[] = {h->Wtm, h->Wt, h->K, h->mu, h->sigma, h->M, h->P, h->I, h->V, h->S[0], h->S[1], h->Sf,
                     h->part_in, h->part_out, h->scale[0], h->scale[1], h->unit_scale,
                     h->mass_in, h->mass_out, h->gram_part, h->mom_part, h->sweeps};
     for (void* p : ptrs)
@@ -174,7 +174,7 @@ int run_project(slime_ca* h, const void* x, const float* x_scale, void* P, void*
     const slime_ca_config& c = h->cfg;
     const int C = h->C;
     WeightPrepArgs w{};
-    w.W = h->W;
+    w.Wtm = h->Wtm;
     w.scale = x_scale;
     w.Wt = h->Wt;
     w.B = c.B;
@@ -283,7 +283,7 @@ int slime_ca_create(const slime_ca_config* config, slime_ca** out) {
     const size_t state_bytes = (size_t)h->state_elems * h->elem;
 
     rc = 0;
-    rc = rc ? rc : dalloc_t(&h->W, (size_t)c.pods * 3 * C * C * 4);
+    rc = rc ? rc : dalloc_t(&h->Wtm, (size_t)c.pods * 3 * C * C * 4);
     rc = rc ? rc : dalloc(&h->Wt, (size_t)c.B * 3 * C * C * h->elem);
     rc = rc ? rc : dalloc_t(&h->K, (size_t)c.pods * c.H * 9 * 4);
     rc = rc ? rc : dalloc_t(&h->mu, n_param_growth(c) * 4);
@@ -339,12 +339,19 @@ int slime_ca_set_params(slime_ca* h, const slime_ca_params* p) {
         return fail(SLIME_EINVAL, "a parameter pointer is NULL");
     const slime_ca_config& c = h->cfg;
     const size_t C = h->C, CC = C * C;
-    // Masters are kept as [pods][plane][C][C] so plane p of pod q is contiguous.
-    for (int q = 0; q < c.pods; ++q) {
-        const float* src[3] = {p->WP, p->WI, p->WV};
-        for (int pl = 0; pl < 3; ++pl)
-            HIP_TRY(hipMemcpy(h->W + ((size_t)q * 3 + pl) * CC, src[pl] + (size_t)q * CC, CC * 4,
+    // Masters are kept transposed, [pods][p*C + n][k], so the per-step weight
+    // preparation reads and writes along k.
+    {
+        std::vector<float> t(3 * CC);
+        for (int q = 0; q < c.pods; ++q) {
+            const float* src[3] = {p->WP + (size_t)q * CC, p->WI + (size_t)q * CC,
+                                   p->WV + (size_t)q * CC};
+            for (int pl = 0; pl < 3; ++pl)
+                for (size_t k = 0; k < C; ++k)
+                    for (size_t n = 0; n < C; ++n) t[(pl * C + n) * C + k] = src[pl][k * C + n];
+            HIP_TRY(hipMemcpy(h->Wtm + (size_t)q * 3 * CC, t.data(), 3 * CC * 4,
                               hipMemcpyHostToDevice));
+        }
     }
     const size_t ng = n_param_growth(c);
     for (size_t i = 0; i < ng; ++i)

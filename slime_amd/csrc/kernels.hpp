@@ -26,10 +26,10 @@ bool gemm_uses_mfma(int dtype, const GemmArgs& a);
 hipError_t launch_gemm(int dtype, const GemmArgs& a, hipStream_t s);
 
 // ---- per-batch scaled, transposed weights -------------------------------------
-// Wt[b][p*C + n][k] = cvt( scale_p(b, k) * W[pod(b)][p][k][n] ), where the mass
-// scale applies only to planes that consume the state (scale[b][k / D]).
+// Wt[b][p*C + n][k] = cvt( scale_p(b, k) * Wtm[pod(b)][p*C + n][k] ), where the
+// mass scale applies only to planes that consume the state (scale[b][k / D]).
 struct WeightPrepArgs {
-    const float* W;       // [pods][nplanes][C][C] fp32 masters
+    const float* Wtm;     // [pods][nplanes*C][C] fp32 masters, already transposed
     const float* scale;   // [B][H] or nullptr
     void* Wt;             // [B][nplanes*C][C]
     int B, C, D, per_pod, nplanes;

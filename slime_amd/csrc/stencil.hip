@@ -26,83 +26,105 @@
 #include "common.hpp"
 #include "kernels.hpp"
 
+#include <type_traits>
+
 namespace slime {
 namespace {
 
 constexpr int kTileY = 4, kTileX = 8;  // tile (cells)
-constexpr int kHaloY = kTileY + 2, kHaloX = kTileX + 2;
-constexpr int kHaloCells = kHaloY * kHaloX;
-constexpr int kTileCells = kTileY * kTileX;
-constexpr int kRun = 4;                // cells per thread along x
+constexpr int kHaloX = kTileX + 2;     // halo rows are 10 cells wide, 6 rows tall
+constexpr int kHaloCells = (kTileY + 2) * kHaloX;  // 60
+constexpr int kHaloPad = 64;           // halo cells reserved per array
+constexpr int kTileCells = kTileY * kTileX;        // 32
+constexpr int kRun = 4;                // cells per thread along x in phase B
 constexpr int kAStride = 12;           // floats per cell in the attention buffer
 
 __device__ __forceinline__ int wrapi(int v, int G) { return v < 0 ? v + G : (v >= G ? v - G : v); }
 
+// Calls f(std::integral_constant<int, R>) for R = R0..N-1: array indices stay
+// compile-time constants, so the staging registers never become a stack array.
+template <int R0, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (R0 < N) {
+        f(std::integral_constant<int, R0>{});
+        static_for<R0 + 1, N>(f);
+    }
+}
+
 template <typename T, int D>
 struct Layout {
-    static constexpr int kCE = 16 / (int)sizeof(T);         // elements per 16-byte chunk
-    static constexpr int kCPR = D / kCE;                    // chunks per (cell, head) row
-    static constexpr int kRowPad = D + kCE;                 // padded row (elements) for I, P
+    static constexpr int kCE = 16 / (int)sizeof(T);          // elements per 16-byte chunk
+    static constexpr int kCPR = D / kCE;                     // chunks per (cell, head) row
+    static constexpr int kRowB = D * (int)sizeof(T);         // bytes per (cell, head) row
+    static constexpr int kSwz = (kCPR < 8 ? kCPR : 8) - 1;   // chunk XOR mask (I and P rows)
     static constexpr int kThreads = (4 * D) < 64 ? 64 : 4 * D;
-    static constexpr int kActive = 4 * D;                   // threads with a (row, pair) task
+    static constexpr int kActive = 4 * D;                    // threads with a phase-B task
     static constexpr int kWaves = kThreads / 64;
-    static constexpr int offX = 0;
-    static constexpr int offV = offX + kHaloCells * D * 4;
-    static constexpr int offI = offV + kHaloCells * D * 4;
-    static constexpr int offP = offI + kHaloCells * kRowPad * (int)sizeof(T);
-    static constexpr int offA = offP + kTileCells * kRowPad * (int)sizeof(T);
-    static constexpr int offR = offA + kTileCells * kAStride * 4;
+    static constexpr int kTPC = kThreads / kTileCells;       // phase-A threads per cell
+    // Staged rows per head: X, V, I halos (64 padded cells each) and the P tile
+    // (padded so that every array spans whole rounds of slots). Every slot loads a
+    // valid address; the padding rows absorb the surplus.
+    static constexpr int kPCells = kThreads / kCPR > kTileCells ? kThreads / kCPR : kTileCells;
+    static constexpr int kSlots = (3 * kHaloPad + kPCells) * kCPR;
+    static constexpr int kRounds = kSlots / kThreads;
+    static_assert(kSlots % kThreads == 0, "slots must fill whole rounds");
+    static constexpr int kBufB = (3 * kHaloPad + kPCells) * kRowB;
+    static constexpr int offX = 0, offV = kHaloPad * kRowB, offI = 2 * kHaloPad * kRowB,
+                         offP = 3 * kHaloPad * kRowB;
+    static constexpr int offA = 2 * kBufB;                   // attention, double-buffered
+    static constexpr int offMS = offA + 2 * kTileCells * kAStride * 4;  // per-cell mu, sigma
+    static constexpr int offR = offMS + 2 * kTileCells * 8 * 4;
     static constexpr int kBytes = offR + kWaves * 16 * 4;
+    // Every array spans whole rounds of slots, so a round's array is a constant.
+    static constexpr int round_array(int r) {
+        return (r * kThreads) / (kHaloPad * kCPR) < 3 ? (r * kThreads) / (kHaloPad * kCPR) : 3;
+    }
+    static_assert((kHaloPad * kCPR) % kThreads == 0, "halo arrays must span whole rounds");
+    // bf16 prefetches the next head into registers during the current one; fp32
+    // (twice the registers per slot) stages each head on demand.
+    static constexpr bool kPrefetch = sizeof(T) == 2;
 };
 
-// Dot product of two padded LDS rows of D channels.
-template <typename T, int D>
-__device__ __forceinline__ float row_dot(const T* a, const T* b) {
-    float acc = 0.f;
+template <typename T>
+__device__ __forceinline__ float2 lds_pair(const unsigned char* p) {
     if constexpr (sizeof(T) == 2) {
-#pragma unroll
-        for (int c = 0; c < D; c += 8) {
-            const uint4 va = *reinterpret_cast<const uint4*>(a + c);
-            const uint4 vb = *reinterpret_cast<const uint4*>(b + c);
-            acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_v, va.x),
-                                                  __builtin_bit_cast(bf16x2_v, vb.x), acc, false);
-            acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_v, va.y),
-                                                  __builtin_bit_cast(bf16x2_v, vb.y), acc, false);
-            acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_v, va.z),
-                                                  __builtin_bit_cast(bf16x2_v, vb.z), acc, false);
-            acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_v, va.w),
-                                                  __builtin_bit_cast(bf16x2_v, vb.w), acc, false);
-        }
+        const uint32_t w = *reinterpret_cast<const uint32_t*>(p);
+        return make_float2(bf16lo(w), bf16hi(w));
     } else {
-#pragma unroll
-        for (int c = 0; c < D; c += 4) {
-            const float4 va = *reinterpret_cast<const float4*>(a + c);
-            const float4 vb = *reinterpret_cast<const float4*>(b + c);
-            acc = __builtin_fmaf(va.x, vb.x, acc);
-            acc = __builtin_fmaf(va.y, vb.y, acc);
-            acc = __builtin_fmaf(va.z, vb.z, acc);
-            acc = __builtin_fmaf(va.w, vb.w, acc);
-        }
+        return *reinterpret_cast<const float2*>(p);
+    }
+}
+
+// Partial dot product of one 16-byte chunk of two rows.
+template <typename T>
+__device__ __forceinline__ float chunk_dot(uint4 a, uint4 b, float acc) {
+    if constexpr (sizeof(T) == 2) {
+        acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_v, a.x),
+                                              __builtin_bit_cast(bf16x2_v, b.x), acc, false);
+        acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_v, a.y),
+                                              __builtin_bit_cast(bf16x2_v, b.y), acc, false);
+        acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_v, a.z),
+                                              __builtin_bit_cast(bf16x2_v, b.z), acc, false);
+        acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_v, a.w),
+                                              __builtin_bit_cast(bf16x2_v, b.w), acc, false);
+    } else {
+        const float4 fa = __builtin_bit_cast(float4, a), fb = __builtin_bit_cast(float4, b);
+        acc = __builtin_fmaf(fa.x, fb.x, acc);
+        acc = __builtin_fmaf(fa.y, fb.y, acc);
+        acc = __builtin_fmaf(fa.z, fb.z, acc);
+        acc = __builtin_fmaf(fa.w, fb.w, acc);
     }
     return acc;
 }
 
-// Converts one 16-byte chunk to fp32 (times s) and writes it to LDS.
-template <typename T>
-__device__ __forceinline__ void chunk_to_f32(float* dst, uint4 v, float s) {
-    if constexpr (sizeof(T) == 2) {
-        float4 lo = make_float4(bf16lo(v.x) * s, bf16hi(v.x) * s, bf16lo(v.y) * s, bf16hi(v.y) * s);
-        float4 hi = make_float4(bf16lo(v.z) * s, bf16hi(v.z) * s, bf16lo(v.w) * s, bf16hi(v.w) * s);
-        reinterpret_cast<float4*>(dst)[0] = lo;
-        reinterpret_cast<float4*>(dst)[1] = hi;
-    } else {
-        float4 f = __builtin_bit_cast(float4, v);
-        f.x *= s;
-        f.y *= s;
-        f.z *= s;
-        f.w *= s;
-        *reinterpret_cast<float4*>(dst) = f;
-    }
+// Sum over groups of kN consecutive lanes (kN = 1, 2, 4 or 8), every lane of the
+// group receiving the sum (DPP quad_perm and row_half_mirror steps).
+template <int kN>
+__device__ __forceinline__ float group_sum(float v) {
+    if constexpr (kN >= 2) v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
+    if constexpr (kN >= 4) v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]
+    if constexpr (kN >= 8) v += dpp_f32<0x141>(v);  // row_half_mirror
+    return v;
 }
 
 // TY: storage type of the unscaled output; fp32 when the caller rescales it into
@@ -114,11 +136,7 @@ __global__ __launch_bounds__((Layout<T, D>::kThreads), 2) void stencil_kernel(St
     constexpr int C = H * D;
     constexpr int kPairs = D / 2;
     extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
-    float* sX = reinterpret_cast<float*>(lds + L::offX);
-    float* sV = reinterpret_cast<float*>(lds + L::offV);
-    T* sI = reinterpret_cast<T*>(lds + L::offI);
-    T* sP = reinterpret_cast<T*>(lds + L::offP);
-    float* sA = reinterpret_cast<float*>(lds + L::offA);
+    float* sMS = reinterpret_cast<float*>(lds + L::offMS);
     float* sR = reinterpret_cast<float*>(lds + L::offR);
 
     const int tid = threadIdx.x;
@@ -132,20 +150,89 @@ __global__ __launch_bounds__((Layout<T, D>::kThreads), 2) void stencil_kernel(St
     const int tile = t % tpb;
     const int ty0 = (tile / tiles_x) * kTileY, tx0 = (tile % tiles_x) * kTileX;
     const int pod = b / a.per_pod;
+    const long long bbase = (long long)b * G * G * C;  // element offset of batch b
 
-    const T* Xg = static_cast<const T*>(a.X);
-    const T* Pg = static_cast<const T*>(a.P);
-    const T* Ig = static_cast<const T*>(a.I);
-    const T* Vg = static_cast<const T*>(a.V);
-    const long long batch_base = (long long)b * G * G;
+    // ---- staging slots: which 16-byte chunk this thread moves for every head -------
+    // Slot q: array q / (64 CPR) (X, V, I halos; then the P tile), cell, chunk. The
+    // same slots serve all heads (+h*D). I and P rows are XOR-swizzled by cell so the
+    // score phase reads them without bank conflicts; X and V rows stay linear.
+    // Slot (round r, thread tid): array L::round_array(r); within the array, row
+    // group j = r mod (rounds per array) covers cells j*kThreads/kCPR + tid/kCPR.
+    // X, V and I share the cell (and the global offset) of a row group.
+    constexpr int kHR = kHaloPad * L::kCPR / L::kThreads;   // rounds per halo array
+    constexpr int kPR = L::kPCells * L::kCPR / L::kThreads; // rounds of the P tile
+    int gofs_h[kHR], lofs_lin[kHR], lofs_swz[kHR], gofs_p[kPR], lofs_p[kPR];
+    {
+        const int ch = tid % L::kCPR;
+#pragma unroll
+        for (int j = 0; j < kHR; ++j) {
+            const int cell = j * (L::kThreads / L::kCPR) + tid / L::kCPR;
+            const int gc = cell < kHaloCells ? cell : kHaloCells - 1;  // padding rows
+            const int gy = wrapi(ty0 + gc / kHaloX - 1, G), gx = wrapi(tx0 + gc % kHaloX - 1, G);
+            gofs_h[j] = (gy * G + gx) * C + ch * L::kCE;
+            lofs_lin[j] = cell * L::kRowB + ch * 16;
+            lofs_swz[j] = cell * L::kRowB + ((ch ^ (cell & L::kSwz)) << 4);
+        }
+#pragma unroll
+        for (int j = 0; j < kPR; ++j) {
+            const int cell = j * (L::kThreads / L::kCPR) + tid / L::kCPR;
+            const int gc = cell < kTileCells ? cell : kTileCells - 1;  // padding rows
+            gofs_p[j] = ((ty0 + gc / kTileX) * G + tx0 + gc % kTileX) * C + ch * L::kCE;
+            lofs_p[j] = L::offP + cell * L::kRowB + ((ch ^ (cell & L::kSwz)) << 4);
+        }
+    }
+    auto slot_g = [&](auto rc) -> int {
+        constexpr int r = decltype(rc)::value, ar = L::round_array(r);
+        if constexpr (ar < 3) return gofs_h[r - ar * kHR];
+        else return gofs_p[r - 3 * kHR];
+    };
+    auto slot_l = [&](auto rc) -> int {
+        constexpr int r = decltype(rc)::value, ar = L::round_array(r);
+        if constexpr (ar < 2) return ar * kHaloPad * L::kRowB + lofs_lin[r - ar * kHR];
+        else if constexpr (ar == 2) return L::offI + lofs_swz[r - 2 * kHR];
+        else return lofs_p[r - 3 * kHR];
+    };
+    const T* srcX = static_cast<const T*>(a.X) + bbase;
+    const T* srcV = static_cast<const T*>(a.V) + bbase;
+    const T* srcI = static_cast<const T*>(a.I) + bbase;
+    const T* srcP = static_cast<const T*>(a.P) + bbase;
+    auto src_of = [&](int ar) -> const T* {
+        return ar == 0 ? srcX : ar == 1 ? srcV : ar == 2 ? srcI : srcP;
+    };
+    u32x4 pre[L::kRounds];
+    auto fetch = [&](int head) {
+        static_for<0, L::kRounds>([&](auto rc) {
+            constexpr int r = decltype(rc)::value;
+            pre[r] = *reinterpret_cast<const u32x4*>(src_of(L::round_array(r)) + slot_g(rc) + head * D);
+        });
+    };
+    if constexpr (L::kPrefetch) fetch(0);
 
-    // Phase-B task: a run of 4 cells of one tile row, two adjacent channels.
+    // Per-cell growth parameters of the whole tile go to LDS once.
+    if (a.per_cell) {
+        for (int i = tid; i < kTileCells * H; i += L::kThreads) {
+            const int cell = i / H, h = i % H;
+            const long long pi =
+                (((long long)pod * G + ty0 + cell / kTileX) * G + tx0 + cell % kTileX) * H + h;
+            sMS[(h * kTileCells + cell) * 2 + 0] = a.mu[pi];
+            sMS[(h * kTileCells + cell) * 2 + 1] = a.sigma[pi];
+        }
+    }
+
+    // ---- phase-B task: a run of 4 cells of one tile row, two adjacent channels ----
     const bool active = tid < L::kActive;
     const int cp = tid % kPairs;
     const int grp = tid / kPairs;  // 0..7 when active
     const int ry = grp >> 1;
     const int rx0 = (grp & 1) * kRun;
     const int c0 = 2 * cp;
+    // LDS byte offset of this thread's pair in halo cell (ry, rx0); a window column
+    // moves by kRowB bytes, a window row by 10 kRowB.
+    const int pbase = (ry * kHaloX + rx0) * L::kRowB + c0 * (int)sizeof(T);
+
+    // ---- phase-A task: one cell, chunk group g of kTPC --------------------------------
+    const int acell = tid / L::kTPC, ag = tid % L::kTPC;
+    const int acy = acell / kTileX, acx = acell % kTileX;
 
     float y[H][kRun][2];
 #pragma unroll
@@ -159,76 +246,60 @@ __global__ __launch_bounds__((Layout<T, D>::kThreads), 2) void stencil_kernel(St
     const float sqrt_log2e = __builtin_sqrtf(kLog2e);
 
     for (int h = 0; h < H; ++h) {
-        const float s_in = a.scale_in ? a.scale_in[b * H + h] : 1.0f;
-        // ---- phase 0: stage the halo tiles of head h --------------------------------
-        constexpr int kHaloChunks = kHaloCells * L::kCPR;
-        constexpr int kTotal = 3 * kHaloChunks + kTileCells * L::kCPR;
-#pragma unroll 2
-        for (int q = tid; q < kTotal; q += L::kThreads) {
-            int arr, cell, ch, gy, gx;
-            if (q < 3 * kHaloChunks) {
-                arr = q / kHaloChunks;
-                const int r = q - arr * kHaloChunks;
-                cell = r / L::kCPR;
-                ch = r - cell * L::kCPR;
-                gy = wrapi(ty0 + cell / kHaloX - 1, G);
-                gx = wrapi(tx0 + cell % kHaloX - 1, G);
-            } else {
-                arr = 3;
-                const int r = q - 3 * kHaloChunks;
-                cell = r / L::kCPR;
-                ch = r - cell * L::kCPR;
-                gy = ty0 + cell / kTileX;
-                gx = tx0 + cell % kTileX;
-            }
-            const long long off = (batch_base + (long long)gy * G + gx) * C + h * D + ch * L::kCE;
-            if (arr == 0) {
-                const uint4 v = *reinterpret_cast<const uint4*>(Xg + off);
-                chunk_to_f32<T>(sX + cell * D + ch * L::kCE, v, s_in);
-            } else if (arr == 1) {
-                const uint4 v = *reinterpret_cast<const uint4*>(Vg + off);
-                chunk_to_f32<T>(sV + cell * D + ch * L::kCE, v, 1.0f);
-            } else if (arr == 2) {
-                *reinterpret_cast<uint4*>(sI + cell * L::kRowPad + ch * L::kCE) =
-                    *reinterpret_cast<const uint4*>(Ig + off);
-            } else {
-                *reinterpret_cast<uint4*>(sP + cell * L::kRowPad + ch * L::kCE) =
-                    *reinterpret_cast<const uint4*>(Pg + off);
-            }
+        unsigned char* buf = lds + (h & 1) * L::kBufB;
+        float* sA = reinterpret_cast<float*>(lds + L::offA) + (h & 1) * kTileCells * kAStride;
+        // ---- stage head h (registers -> LDS), then prefetch head h+1 ------------------
+        if constexpr (!L::kPrefetch) fetch(h);
+        static_for<0, L::kRounds>([&](auto rc) {
+            constexpr int r = decltype(rc)::value;
+            *reinterpret_cast<u32x4*>(buf + slot_l(rc)) = pre[r];
+        });
+        if constexpr (L::kPrefetch) {
+            if (h + 1 < H) fetch(h + 1);
         }
         __syncthreads();
 
-        // ---- phase A: attention scores (S4), k-major so lanes walk adjacent cells --
-#pragma unroll 1
-        for (int i = tid; i < 9 * kTileCells; i += L::kThreads) {
-            const int k = i / kTileCells, cell = i % kTileCells;
-            const int cy = cell / kTileX, cx = cell % kTileX;
-            const int nb = (cy + k / 3) * kHaloX + (cx + k % 3);
-            sA[cell * kAStride + k] =
-                row_dot<T, D>(sP + cell * L::kRowPad, sI + nb * L::kRowPad) * inv_sqrt_d;
-        }
-        __syncthreads();
-#pragma unroll 1
-        for (int cell = tid; cell < kTileCells; cell += L::kThreads) {
-            float* s = sA + cell * kAStride;
-            float m = s[0];
+        // ---- phase A: attention scores (S4) and softmax --------------------------------
+        {
+            float s[9];
 #pragma unroll
-            for (int k = 1; k < 9; ++k) m = fmaxf(m, s[k]);
-            float e[9], sum = 0.f;
+            for (int k = 0; k < 9; ++k) s[k] = 0.f;
+#pragma unroll
+            for (int c = ag; c < L::kCPR; c += L::kTPC) {
+                const uint4 pv = *reinterpret_cast<const uint4*>(
+                    buf + L::offP + acell * L::kRowB + ((c ^ (acell & L::kSwz)) << 4));
+#pragma unroll
+                for (int k = 0; k < 9; ++k) {
+                    const int nb = (acy + k / 3) * kHaloX + acx + k % 3;
+                    const uint4 iv = *reinterpret_cast<const uint4*>(
+                        buf + L::offI + nb * L::kRowB + ((c ^ (nb & L::kSwz)) << 4));
+                    s[k] = chunk_dot<T>(pv, iv, s[k]);
+                }
+            }
+            float m = -3.0e38f;
 #pragma unroll
             for (int k = 0; k < 9; ++k) {
-                e[k] = exp2_fast((s[k] - m) * kLog2e);
-                sum += e[k];
+                s[k] = group_sum<L::kTPC>(s[k]) * inv_sqrt_d;
+                m = fmaxf(m, s[k]);
+            }
+            float sum = 0.f;
+#pragma unroll
+            for (int k = 0; k < 9; ++k) {
+                s[k] = exp2_fast((s[k] - m) * kLog2e);
+                sum += s[k];
             }
             const float inv = 1.0f / sum;
+            if (ag == 0) {
 #pragma unroll
-            for (int k = 0; k < 9; ++k) s[k] = e[k] * inv;
+                for (int k = 0; k < 9; ++k) sA[acell * kAStride + k] = s[k] * inv;
+            }
         }
         __syncthreads();
 
-        // ---- phase B: potential, growth, propagation, update, head mixing --------
+        // ---- phase B: potential, growth, propagation, update, head mixing --------------
         float xacc = 0.f;
         if (active) {
+            const float s_in = a.scale_in ? a.scale_in[b * H + h] : 1.0f;
             float kw[9];
 #pragma unroll
             for (int k = 0; k < 9; ++k) kw[k] = a.K[(pod * H + h) * 9 + k];
@@ -241,23 +312,25 @@ __global__ __launch_bounds__((Layout<T, D>::kThreads), 2) void stencil_kernel(St
                 gb = a.mu[pod * H + h] * ga;
             }
             const float dt = a.dt, two_dt = 2.0f * a.dt;
+            const unsigned char* px = buf + L::offX + pbase;
+            const unsigned char* pvv = buf + L::offV + pbase;
 
             float2 xw[3][3], vw[3][3];
 #pragma unroll
             for (int dy = 0; dy < 3; ++dy)
 #pragma unroll
                 for (int dx = 0; dx < 2; ++dx) {
-                    const int hc = (ry + dy) * kHaloX + rx0 + dx;
-                    xw[dy][dx] = *reinterpret_cast<const float2*>(sX + hc * D + c0);
-                    vw[dy][dx] = *reinterpret_cast<const float2*>(sV + hc * D + c0);
+                    const int o = (dy * kHaloX + dx) * L::kRowB;
+                    xw[dy][dx] = lds_pair<T>(px + o);
+                    vw[dy][dx] = lds_pair<T>(pvv + o);
                 }
 #pragma unroll
             for (int x = 0; x < kRun; ++x) {
 #pragma unroll
                 for (int dy = 0; dy < 3; ++dy) {
-                    const int hc = (ry + dy) * kHaloX + rx0 + x + 2;
-                    xw[dy][2] = *reinterpret_cast<const float2*>(sX + hc * D + c0);
-                    vw[dy][2] = *reinterpret_cast<const float2*>(sV + hc * D + c0);
+                    const int o = (dy * kHaloX + x + 2) * L::kRowB;
+                    xw[dy][2] = lds_pair<T>(px + o);
+                    vw[dy][2] = lds_pair<T>(pvv + o);
                 }
                 const float* ap = sA + (ry * kTileX + rx0 + x) * kAStride;
                 const float4 a0 = reinterpret_cast<const float4*>(ap)[0];
@@ -265,10 +338,10 @@ __global__ __launch_bounds__((Layout<T, D>::kThreads), 2) void stencil_kernel(St
                 const float a8 = ap[8];
                 const float aw[9] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w, a8};
                 if (a.per_cell) {
-                    const long long pi =
-                        (((long long)pod * G + ty0 + ry) * G + tx0 + rx0 + x) * H + h;
-                    ga = sqrt_log2e / (a.sigma[pi] + 1e-7f);
-                    gb = a.mu[pi] * ga;
+                    const int cell = ry * kTileX + rx0 + x;
+                    const float2 ms = *reinterpret_cast<const float2*>(sMS + (h * kTileCells + cell) * 2);
+                    ga = sqrt_log2e / (ms.y + 1e-7f);
+                    gb = ms.x * ga;
                 }
                 float z[2];
 #pragma unroll
@@ -281,10 +354,10 @@ __global__ __launch_bounds__((Layout<T, D>::kThreads), 2) void stencil_kernel(St
                         u = __builtin_fmaf(kw[k], e ? xv.y : xv.x, u);
                         vt = __builtin_fmaf(aw[k], e ? vv.y : vv.x, vt);
                     }
-                    const float tg = __builtin_fmaf(u, ga, -gb);
+                    const float tg = __builtin_fmaf(u * s_in, ga, -gb);
                     const float ex = exp2_fast(-tg * tg);
                     const float coef = __builtin_fmaf(ex, two_dt, -dt);  // dt * g
-                    const float xc = e ? xw[1][1].y : xw[1][1].x;
+                    const float xc = (e ? xw[1][1].y : xw[1][1].x) * s_in;
                     z[e] = __builtin_fmaf(coef, vt, xc);
                     xacc += xc;
                 }
@@ -300,18 +373,19 @@ __global__ __launch_bounds__((Layout<T, D>::kThreads), 2) void stencil_kernel(St
                     vw[dy][0] = vw[dy][1];
                     vw[dy][1] = vw[dy][2];
                 }
-                // Keep the scheduler from hoisting later columns' LDS reads over
-                // this cell: the 128 output accumulators already need half the
-                // register budget of a 2-waves-per-SIMD launch.
+                // Keep the scheduler from hoisting later cells' LDS reads over this
+                // one: the output accumulators and the staging registers already
+                // take most of a 2-waves-per-SIMD register budget.
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
 #pragma unroll
         for (int j = 0; j < H; ++j) xin[j] = (j == h) ? xacc : xin[j];
-        __syncthreads();  // LDS is restaged for the next head
+        // No barrier here: the next head stages into the other LDS buffer, and the
+        // barrier after that staging orders this head's reads before any reuse.
     }
 
-    // ---- phase C: store Y (storage type) and the tile's mass partial sums ---------
+    // ---- phase C: store Y and the tile's mass partial sums ------------------------------
     TY* Yg = static_cast<TY*>(a.Y);
     float ysum[H];
 #pragma unroll
@@ -319,7 +393,7 @@ __global__ __launch_bounds__((Layout<T, D>::kThreads), 2) void stencil_kernel(St
     if (active) {
 #pragma unroll
         for (int x = 0; x < kRun; ++x) {
-            const long long base = (batch_base + (long long)(ty0 + ry) * G + tx0 + rx0 + x) * C + c0;
+            const long long base = bbase + ((long long)(ty0 + ry) * G + tx0 + rx0 + x) * C + c0;
 #pragma unroll
             for (int o = 0; o < H; ++o) {
                 const float r0 = Store<TY>::round(y[o][x][0]);
@@ -341,11 +415,11 @@ __global__ __launch_bounds__((Layout<T, D>::kThreads), 2) void stencil_kernel(St
     }
     __syncthreads();
     if (tid < 2 * H) {
-        float s = 0.f;
-        for (int w = 0; w < L::kWaves; ++w) s += sR[w * 16 + tid];
+        float sum = 0.f;
+        for (int w = 0; w < L::kWaves; ++w) sum += sR[w * 16 + tid];
         const int j = tid % H;
         float* dst = tid < H ? a.part_in : a.part_out;
-        dst[((long long)b * H + j) * tpb + tile] = s;
+        dst[((long long)b * H + j) * tpb + tile] = sum;
     }
 }
 
