@@ -61,29 +61,36 @@ struct Layout {
     static constexpr int kActive = 4 * D;                    // threads with a phase-B task
     static constexpr int kWaves = kThreads / 64;
     static constexpr int kTPC = kThreads / kTileCells;       // phase-A threads per cell
-    // Staged rows per head: X, V, I halos (64 padded cells each) and the P tile
-    // (padded so that every array spans whole rounds of slots). Every slot loads a
-    // valid address; the padding rows absorb the surplus.
-    static constexpr int kPCells = kThreads / kCPR > kTileCells ? kThreads / kCPR : kTileCells;
-    static constexpr int kSlots = (3 * kHaloPad + kPCells) * kCPR;
-    static constexpr int kRounds = kSlots / kThreads;
-    static_assert(kSlots % kThreads == 0, "slots must fill whole rounds");
+    // Direct global->LDS staging: one wave instruction fills 1 KiB = kCPI rows.
+    static constexpr int kCPI = 64 / kCPR;                   // cells per DMA instruction
+    static constexpr int kPCells = kCPI > kTileCells ? kCPI : kTileCells;  // P rows (padded)
+    static constexpr int kHG = kHaloPad / kCPI;              // instruction groups per halo array
+    static constexpr int kPG = kPCells / kCPI;               // instruction groups of the P tile
+    static constexpr int kIA = kHG / kWaves;                 // per wave, per halo array
+    static constexpr int kPA = kPG / kWaves;                 // per wave, P tile
+    static_assert(kHG % kWaves == 0 && kPG % kWaves == 0, "DMA groups must split over waves");
     static constexpr int kBufB = (3 * kHaloPad + kPCells) * kRowB;
     static constexpr int offX = 0, offV = kHaloPad * kRowB, offI = 2 * kHaloPad * kRowB,
                          offP = 3 * kHaloPad * kRowB;
-    static constexpr int offA = 2 * kBufB;                   // attention, double-buffered
-    static constexpr int offMS = offA + 2 * kTileCells * kAStride * 4;  // per-cell mu, sigma
-    static constexpr int offR = offMS + 2 * kTileCells * 8 * 4;
-    static constexpr int kBytes = offR + kWaves * 16 * 4;
-    // Every array spans whole rounds of slots, so a round's array is a constant.
-    static constexpr int round_array(int r) {
-        return (r * kThreads) / (kHaloPad * kCPR) < 3 ? (r * kThreads) / (kHaloPad * kCPR) : 3;
-    }
-    static_assert((kHaloPad * kCPR) % kThreads == 0, "halo arrays must span whole rounds");
-    // bf16 prefetches the next head into registers during the current one; fp32
-    // (twice the registers per slot) stages each head on demand.
-    static constexpr bool kPrefetch = sizeof(T) == 2;
 };
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) const void gbl_void_t;
+
+__device__ __forceinline__ void wait_vm0() {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // s_waitcnt vmcnt(0)
+}
+
+// Workgroup barrier for LDS data only. __syncthreads() also waits for every
+// outstanding vector-memory operation (its release fence covers the direct
+// loads still landing in the other staging buffer); this waits for this wave's
+// LDS operations (lgkmcnt(0)) and then meets the other waves at s_barrier.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // s_waitcnt lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
 
 template <typename T>
 __device__ __forceinline__ float2 lds_pair(const unsigned char* p) {
@@ -135,11 +142,16 @@ __global__ __launch_bounds__((Layout<T, D>::kThreads), 2) void stencil_kernel(St
     constexpr int H = kHeads;
     constexpr int C = H * D;
     constexpr int kPairs = D / 2;
-    extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
-    float* sMS = reinterpret_cast<float*>(lds + L::offMS);
-    float* sR = reinterpret_cast<float*>(lds + L::offR);
+    // Two staging buffers as separate LDS objects: the compiler can then tell that
+    // reading one does not depend on the direct loads landing in the other.
+    __shared__ __attribute__((aligned(16))) unsigned char bufA[L::kBufB];
+    __shared__ __attribute__((aligned(16))) unsigned char bufB[L::kBufB];
+    __shared__ __attribute__((aligned(16))) float sAtt[2][kTileCells * kAStride];
+    __shared__ __attribute__((aligned(16))) float sMS[H * kTileCells * 2];
+    __shared__ float sR[L::kWaves * 16];
 
     const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
     const int G = a.G;
     const int tiles_x = G / kTileX;
     const int tpb = (G / kTileY) * tiles_x;
@@ -152,63 +164,74 @@ __global__ __launch_bounds__((Layout<T, D>::kThreads), 2) void stencil_kernel(St
     const int pod = b / a.per_pod;
     const long long bbase = (long long)b * G * G * C;  // element offset of batch b
 
-    // ---- staging slots: which 16-byte chunk this thread moves for every head -------
-    // Slot q: array q / (64 CPR) (X, V, I halos; then the P tile), cell, chunk. The
-    // same slots serve all heads (+h*D). I and P rows are XOR-swizzled by cell so the
-    // score phase reads them without bank conflicts; X and V rows stay linear.
-    // Slot (round r, thread tid): array L::round_array(r); within the array, row
-    // group j = r mod (rounds per array) covers cells j*kThreads/kCPR + tid/kCPR.
-    // X, V and I share the cell (and the global offset) of a row group.
-    constexpr int kHR = kHaloPad * L::kCPR / L::kThreads;   // rounds per halo array
-    constexpr int kPR = L::kPCells * L::kCPR / L::kThreads; // rounds of the P tile
-    int gofs_h[kHR], lofs_lin[kHR], lofs_swz[kHR], gofs_p[kPR], lofs_p[kPR];
+    // ---- direct global->LDS staging of one head --------------------------------------
+    // Lane l of a DMA instruction covering cells g*kCPI .. +kCPI lands at row
+    // g*kCPI + l/kCPR, physical chunk l%kCPR. X and V rows are stored linearly; I
+    // and P rows are XOR-swizzled by cell (the score phase reads whole rows of
+    // neighbouring cells), so those lanes fetch logical chunk (l%kCPR) ^ (cell&kSwz).
+    // Wave w issues groups g = w + k*kWaves. Per-lane element offsets, head 0:
+    int hoff_lin[L::kIA], hoff_swz[L::kIA], poff[L::kPA];
     {
-        const int ch = tid % L::kCPR;
+        const int ch = lane % L::kCPR;
 #pragma unroll
-        for (int j = 0; j < kHR; ++j) {
-            const int cell = j * (L::kThreads / L::kCPR) + tid / L::kCPR;
+        for (int k = 0; k < L::kIA; ++k) {
+            const int cell = (wave + k * L::kWaves) * L::kCPI + lane / L::kCPR;
             const int gc = cell < kHaloCells ? cell : kHaloCells - 1;  // padding rows
             const int gy = wrapi(ty0 + gc / kHaloX - 1, G), gx = wrapi(tx0 + gc % kHaloX - 1, G);
-            gofs_h[j] = (gy * G + gx) * C + ch * L::kCE;
-            lofs_lin[j] = cell * L::kRowB + ch * 16;
-            lofs_swz[j] = cell * L::kRowB + ((ch ^ (cell & L::kSwz)) << 4);
+            const int base = (gy * G + gx) * C;
+            hoff_lin[k] = base + ch * L::kCE;
+            hoff_swz[k] = base + (ch ^ (cell & L::kSwz)) * L::kCE;
         }
 #pragma unroll
-        for (int j = 0; j < kPR; ++j) {
-            const int cell = j * (L::kThreads / L::kCPR) + tid / L::kCPR;
+        for (int k = 0; k < L::kPA; ++k) {
+            const int cell = (wave + k * L::kWaves) * L::kCPI + lane / L::kCPR;
             const int gc = cell < kTileCells ? cell : kTileCells - 1;  // padding rows
-            gofs_p[j] = ((ty0 + gc / kTileX) * G + tx0 + gc % kTileX) * C + ch * L::kCE;
-            lofs_p[j] = L::offP + cell * L::kRowB + ((ch ^ (cell & L::kSwz)) << 4);
+            poff[k] = ((ty0 + gc / kTileX) * G + tx0 + gc % kTileX) * C +
+                      (ch ^ (cell & L::kSwz)) * L::kCE;
         }
     }
-    auto slot_g = [&](auto rc) -> int {
-        constexpr int r = decltype(rc)::value, ar = L::round_array(r);
-        if constexpr (ar < 3) return gofs_h[r - ar * kHR];
-        else return gofs_p[r - 3 * kHR];
-    };
-    auto slot_l = [&](auto rc) -> int {
-        constexpr int r = decltype(rc)::value, ar = L::round_array(r);
-        if constexpr (ar < 2) return ar * kHaloPad * L::kRowB + lofs_lin[r - ar * kHR];
-        else if constexpr (ar == 2) return L::offI + lofs_swz[r - 2 * kHR];
-        else return lofs_p[r - 3 * kHR];
-    };
     const T* srcX = static_cast<const T*>(a.X) + bbase;
     const T* srcV = static_cast<const T*>(a.V) + bbase;
     const T* srcI = static_cast<const T*>(a.I) + bbase;
     const T* srcP = static_cast<const T*>(a.P) + bbase;
-    auto src_of = [&](int ar) -> const T* {
-        return ar == 0 ? srcX : ar == 1 ? srcV : ar == 2 ? srcI : srcP;
+    auto issue_head = [&](int h, unsigned char* buf) {
+#pragma unroll
+        for (int k = 0; k < L::kIA; ++k) {
+            unsigned char* row = buf + (wave + k * L::kWaves) * 1024;
+            __builtin_amdgcn_global_load_lds((gbl_void_t*)(srcX + hoff_lin[k] + h * D),
+                                             (lds_void_t*)(row + L::offX), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((gbl_void_t*)(srcV + hoff_lin[k] + h * D),
+                                             (lds_void_t*)(row + L::offV), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((gbl_void_t*)(srcI + hoff_swz[k] + h * D),
+                                             (lds_void_t*)(row + L::offI), 16, 0, 0);
+        }
+#pragma unroll
+        for (int k = 0; k < L::kPA; ++k)
+            __builtin_amdgcn_global_load_lds((gbl_void_t*)(srcP + poff[k] + h * D),
+                                             (lds_void_t*)(buf + L::offP + (wave + k * L::kWaves) * 1024),
+                                             16, 0, 0);
     };
-    u32x4 pre[L::kRounds];
-    auto fetch = [&](int head) {
-        static_for<0, L::kRounds>([&](auto rc) {
-            constexpr int r = decltype(rc)::value;
-            pre[r] = *reinterpret_cast<const u32x4*>(src_of(L::round_array(r)) + slot_g(rc) + head * D);
-        });
-    };
-    if constexpr (L::kPrefetch) fetch(0);
 
-    // Per-cell growth parameters of the whole tile go to LDS once.
+    // Per-head parameters (and per-cell growth parameters) go to LDS once, before
+    // any direct load is issued: reading them later from global memory would make
+    // the in-order vector-memory counter wait for the next head's staging.
+    __shared__ float sK[H * 9], sMW[H * H], sGa[H], sGb[H], sScale[H];
+    {
+        constexpr float kLog2eP = 1.4426950408889634f;
+        for (int i = tid; i < H * 9; i += L::kThreads) sK[i] = a.K[pod * H * 9 + i];
+        for (int i = tid; i < H * H; i += L::kThreads) {
+            const int hh = i / H, o = i % H;  // sMW[h][o] = M[o][h]
+            sMW[i] = a.M[(pod * H + o) * H + hh];
+        }
+        if (tid < H) {
+            sScale[tid] = a.scale_in ? a.scale_in[b * H + tid] : 1.0f;
+            if (!a.per_cell) {
+                const float ga = __builtin_sqrtf(kLog2eP) / (a.sigma[pod * H + tid] + 1e-7f);
+                sGa[tid] = ga;
+                sGb[tid] = a.mu[pod * H + tid] * ga;
+            }
+        }
+    }
     if (a.per_cell) {
         for (int i = tid; i < kTileCells * H; i += L::kThreads) {
             const int cell = i / H, h = i % H;
@@ -218,6 +241,7 @@ __global__ __launch_bounds__((Layout<T, D>::kThreads), 2) void stencil_kernel(St
             sMS[(h * kTileCells + cell) * 2 + 1] = a.sigma[pi];
         }
     }
+    issue_head(0, bufA);
 
     // ---- phase-B task: a run of 4 cells of one tile row, two adjacent channels ----
     const bool active = tid < L::kActive;
@@ -245,19 +269,11 @@ __global__ __launch_bounds__((Layout<T, D>::kThreads), 2) void stencil_kernel(St
     constexpr float kLog2e = 1.4426950408889634f;
     const float sqrt_log2e = __builtin_sqrtf(kLog2e);
 
-    for (int h = 0; h < H; ++h) {
-        unsigned char* buf = lds + (h & 1) * L::kBufB;
-        float* sA = reinterpret_cast<float*>(lds + L::offA) + (h & 1) * kTileCells * kAStride;
-        // ---- stage head h (registers -> LDS), then prefetch head h+1 ------------------
-        if constexpr (!L::kPrefetch) fetch(h);
-        static_for<0, L::kRounds>([&](auto rc) {
-            constexpr int r = decltype(rc)::value;
-            *reinterpret_cast<u32x4*>(buf + slot_l(rc)) = pre[r];
-        });
-        if constexpr (L::kPrefetch) {
-            if (h + 1 < H) fetch(h + 1);
-        }
-        __syncthreads();
+    auto do_head = [&](int h, const unsigned char* buf, unsigned char* nxt) {
+        float* sA = sAtt[h & 1];
+        wait_vm0();       // this wave's loads of head h have landed
+        __syncthreads();  // ... and every other wave's; head h-1 is fully consumed
+        if (h + 1 < H) issue_head(h + 1, nxt);
 
         // ---- phase A: attention scores (S4) and softmax --------------------------------
         {
@@ -294,22 +310,22 @@ __global__ __launch_bounds__((Layout<T, D>::kThreads), 2) void stencil_kernel(St
                 for (int k = 0; k < 9; ++k) sA[acell * kAStride + k] = s[k] * inv;
             }
         }
-        __syncthreads();
+        lds_barrier();
 
         // ---- phase B: potential, growth, propagation, update, head mixing --------------
         float xacc = 0.f;
         if (active) {
-            const float s_in = a.scale_in ? a.scale_in[b * H + h] : 1.0f;
+            const float s_in = sScale[h];
             float kw[9];
 #pragma unroll
-            for (int k = 0; k < 9; ++k) kw[k] = a.K[(pod * H + h) * 9 + k];
+            for (int k = 0; k < 9; ++k) kw[k] = sK[h * 9 + k];
             float mw[H];
 #pragma unroll
-            for (int o = 0; o < H; ++o) mw[o] = a.M[(pod * H + o) * H + h];
+            for (int o = 0; o < H; ++o) mw[o] = sMW[h * H + o];
             float ga = 0.f, gb = 0.f;
             if (!a.per_cell) {
-                ga = sqrt_log2e / (a.sigma[pod * H + h] + 1e-7f);
-                gb = a.mu[pod * H + h] * ga;
+                ga = sGa[h];
+                gb = sGb[h];
             }
             const float dt = a.dt, two_dt = 2.0f * a.dt;
             const unsigned char* px = buf + L::offX + pbase;
@@ -374,15 +390,17 @@ __global__ __launch_bounds__((Layout<T, D>::kThreads), 2) void stencil_kernel(St
                     vw[dy][1] = vw[dy][2];
                 }
                 // Keep the scheduler from hoisting later cells' LDS reads over this
-                // one: the output accumulators and the staging registers already
-                // take most of a 2-waves-per-SIMD register budget.
+                // one: the output accumulators already take a large share of a
+                // 2-waves-per-SIMD register budget.
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
 #pragma unroll
         for (int j = 0; j < H; ++j) xin[j] = (j == h) ? xacc : xin[j];
-        // No barrier here: the next head stages into the other LDS buffer, and the
-        // barrier after that staging orders this head's reads before any reuse.
+    };
+    for (int h = 0; h < H; h += 2) {
+        do_head(h, bufA, bufB);
+        do_head(h + 1, bufB, bufA);
     }
 
     // ---- phase C: store Y and the tile's mass partial sums ------------------------------
@@ -403,7 +421,6 @@ __global__ __launch_bounds__((Layout<T, D>::kThreads), 2) void stencil_kernel(St
             }
         }
     }
-    const int lane = tid & 63, wave = tid >> 6;
 #pragma unroll
     for (int j = 0; j < H; ++j) {
         const float sx = wave_sum(xin[j]);
@@ -426,16 +443,8 @@ __global__ __launch_bounds__((Layout<T, D>::kThreads), 2) void stencil_kernel(St
 template <typename T, int D, typename TY>
 hipError_t launch_tdy(const StencilArgs& a, hipStream_t s) {
     using L = Layout<T, D>;
-    static bool attr_set = false;
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void*)stencil_kernel<T, D, TY>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, L::kBytes);
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
     const int tiles = (a.G / kTileY) * (a.G / kTileX);
-    hipLaunchKernelGGL((stencil_kernel<T, D, TY>), dim3(a.B * tiles), dim3(L::kThreads), L::kBytes,
-                       s, a);
+    hipLaunchKernelGGL((stencil_kernel<T, D, TY>), dim3(a.B * tiles), dim3(L::kThreads), 0, s, a);
     return hipGetLastError();
 }
 
