@@ -117,7 +117,25 @@ __device__ __forceinline__ void store_tile_bf16(const f32x16 (&acc)[4][4], bf16_
 }
 
 typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(1))) const void gbl_void_t;
+
+// One direct global->LDS load (global_load_lds_dwordx4): 16 bytes per lane from
+// gaddr land at LDS byte address lds_base + 16 * lane. Issued through inline asm:
+// the compiler would otherwise make every later LDS read wait for all such loads
+// still in flight (it cannot tell which stage they fill). The pipeline waits for
+// each slab itself (wait_vm) before the barrier that publishes it.
+__device__ __forceinline__ void dma16(const void* gaddr, unsigned lds_base) {
+    asm volatile(
+        "s_mov_b32 m0, %0\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, off"
+        :
+        : "s"(lds_base), "v"(gaddr)
+        : "memory", "m0");
+}
+
+__device__ __forceinline__ unsigned lds_addr(const void* p) {
+    return (unsigned)(size_t)(const lds_void_t*)p;
+}
 
 // Issues the direct global->LDS loads of slab ks of a tile into one stage. A wave
 // instruction fills 1 KiB of LDS = 16 tile rows of 64 bytes: lane l lands at row
@@ -138,17 +156,16 @@ __device__ __forceinline__ void issue_slab(const GemmArgs& g, int tile, int nN, 
     const int chunk = (lane & 3) ^ ((lane >> 3) & 3);
     const unsigned lane_off = (unsigned)((sub * K + chunk * kE) * (long long)sizeof(T));
     const unsigned row_bytes = (unsigned)(K * sizeof(T));
+    const unsigned sbase = lds_addr(stage);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int R = (4 * j + wave) * 16;
-        __builtin_amdgcn_global_load_lds((gbl_void_t*)(a + R * row_bytes + lane_off),
-                                         (lds_void_t*)(stage + R * kSlabB), 16, 0, 0);
+        dma16(a + R * row_bytes + lane_off, sbase + R * kSlabB);
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int R = (4 * j + wave) * 16;
-        __builtin_amdgcn_global_load_lds((gbl_void_t*)(b + R * row_bytes + lane_off),
-                                         (lds_void_t*)(stage + (kBM + R) * kSlabB), 16, 0, 0);
+        dma16(b + R * row_bytes + lane_off, sbase + (kBM + R) * kSlabB);
     }
 }
 constexpr int kDmaPerSlab = 8;  // DMA instructions per wave per slab
@@ -173,6 +190,16 @@ __device__ __forceinline__ void wait_vm(int n) {
 // contiguous range. Slab s of every tile lives in stage s % 4; slabs of the next
 // tile are fetched while the current tile finishes, so tiles follow each other
 // with only the epilogue in between.
+// Workgroup barrier for LDS data only: __syncthreads() would also wait for every
+// outstanding vector-memory operation (its release fence covers the direct loads
+// of later slabs and the previous tile's stores), draining the pipeline.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // s_waitcnt lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 template <typename T>
 __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs g) {
     __shared__ __attribute__((aligned(16))) unsigned char st0[kStageB];
@@ -185,7 +212,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs g) {
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar LDS addresses
     const int wm = wave & 1, wn = wave >> 1;
     const int r32 = lane & 31, half = lane >> 5;
 
@@ -239,7 +266,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs g) {
                 int younger = (has1 ? kDmaPerSlab : 0) + (has2 ? kDmaPerSlab : 0);
                 if (stores_pending && kt < kAhead) younger = kStores <= 32 ? younger + kStores : 0;
                 wait_vm(younger);
-                __syncthreads();  // every wave's part of slab kt is in LDS; slab kt-1 is consumed
+                lds_barrier();  // every wave's part of slab kt is in LDS; slab kt-1 is consumed
                 // Refill the stage of slab kt-1 with slab kt+3 (this tile or the next).
                 if (kt + kAhead < nk)
                     issue_slab<T>(g, tile, nN, kt + kAhead, wave, lane, fill);
@@ -288,7 +315,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs g) {
         if constexpr (kBf16) {
             // The last slab's stage (3) is free once every wave has read it; the
             // other three are receiving the next tile's first slabs.
-            __syncthreads();
+            lds_barrier();
             unsigned char* ep = st3 + wave * kEpiWaveB;
             bf16_t* obase = reinterpret_cast<bf16_t*>(out) + (long long)(m0 + wm * 128) * g.ncol + col0;
             switch (g.act[plane]) {

@@ -151,7 +151,8 @@ __global__ __launch_bounds__((Layout<T, D>::kThreads), 2) void stencil_kernel(St
     __shared__ float sR[L::kWaves * 16];
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar LDS addresses
     const int G = a.G;
     const int tiles_x = G / kTileX;
     const int tpb = (G / kTileY) * tiles_x;
