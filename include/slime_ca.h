@@ -22,7 +22,10 @@
  *   slime_ca_field_from_state               initialize_ca_from_field_kernel /
  *                                           update_field_from_ca_kernel
  *                                           (slime/core/organism.cu:691-743)
- *   slime_ca_last_error                     the printed message of CUDA_CHECK
+ *   slime_neural_ca_update                  neural_ca_update_kernel, the organism's
+ *                                           per-generation CA call
+ *                                           (slime/core/organism.cu:617-688)
+ *   slime_ca_last_error                    the printed message of CUDA_CHECK
  *                                           (slime/runtime.cu:11-20), returned instead
  *                                           of exit(1)
  *
@@ -124,6 +127,34 @@ int slime_ca_fitness_sweeps(slime_ca* ca, int* h_sweeps);
  * X[y][x][c] = conc[y][x] * sin(0.1 c), and conc[y][x] = mean_c X[y][x][c]. */
 int slime_ca_init_from_field(slime_ca* ca, const float* conc, void* x, void* stream);
 int slime_ca_field_from_state(slime_ca* ca, const void* x, float* conc, void* stream);
+
+/* The buffers of the reference's MultiHeadCAState (slime/core/pseudopod.cu:29-38)
+ * that one organism generation reads and writes, under the same field names. The
+ * parameter fields of that struct (perception_weights, interaction_weights,
+ * value_weights, head_mixing_weights, flow_kernels) are held by the handle and
+ * uploaded by slime_ca_set_params, which replaces init_multihead_ca_kernel. */
+typedef struct {
+    float* mass_buffer; /* device, H floats: per-head mass after conservation (may be NULL) */
+    void* ca_input;     /* device [G][G][C], handle dtype */
+    void* ca_output;    /* device [G][G][C], handle dtype, distinct from ca_input */
+} slime_multihead_ca_state;
+
+/* One organism generation of the CA, launched from the host on `stream`; replaces
+ * neural_ca_update_kernel (slime/core/organism.cu:617-688) for a handle with B = 1:
+ *   ca_input  = initialize_ca_from_field(chemical_concentration)
+ *   ca_output = one step S1-S7 of ca_input (projections, flow Lenia, head mixing and
+ *               mass conservation)
+ *   chemical_concentration = update_field_from_ca(ca_output)
+ *   mass_buffer[h] = conserved mass of head h
+ *   effective_rank_history[generation] = mean over heads of the effective rank of
+ *               ca_output's per-head Gram matrix (E1-E3), in place of the
+ *               weight-energy proxy compute_effective_rank_kernel
+ *               (slime/core/pseudopod.cu:302-345).
+ * chemical_concentration is device [G][G] fp32; effective_rank_history is a device
+ * float array of more than `generation` entries. */
+int slime_neural_ca_update(slime_ca* ca, const slime_multihead_ca_state* state,
+                           float* chemical_concentration, float* effective_rank_history,
+                           int generation, void* stream);
 
 /* Kernel timing (no counterpart in the reference, which has no timers on this
  * path). While enabled, slime_ca_step records HIP events on its stream around

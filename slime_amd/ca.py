@@ -198,6 +198,37 @@ class Pseudopod:
         _lib.check(self.lib.slime_ca_init_from_field(self._h, _ptr(conc), _ptr(x), _stream(stream)))
         return x
 
+    def neural_ca_update(self, conc, ca_input, ca_output, erank_history, generation: int,
+                         mass_buffer=None, stream=None):
+        """One organism generation (neural_ca_update_kernel, slime/core/organism.cu:617-688)
+        on a B = 1 handle: ``ca_input`` <- field, ``ca_output`` <- one step,
+        ``conc`` <- mean over channels of ``ca_output`` (updated in place),
+        ``erank_history[generation]`` <- mean per-head effective rank of ``ca_output``,
+        ``mass_buffer`` (optional, [H] fp32) <- per-head conserved mass."""
+        torch = _torch()
+        shape = (self.G, self.G, self.C)
+        for t, n in ((ca_input, "ca_input"), (ca_output, "ca_output")):
+            if tuple(t.shape) != shape or t.dtype != self.torch_dtype or not t.is_cuda \
+                    or not t.is_contiguous():
+                raise ValueError(f"{n} must be a contiguous CUDA {self.torch_dtype} tensor of "
+                                 f"shape {shape}")
+        for t, n, shp in ((conc, "conc", (self.G, self.G)),
+                          (erank_history, "erank_history", None),
+                          (mass_buffer, "mass_buffer", (self.H,))):
+            if t is None and n == "mass_buffer":
+                continue
+            if t.dtype != torch.float32 or not t.is_cuda or not t.is_contiguous() \
+                    or (shp is not None and tuple(t.shape) != shp):
+                raise ValueError(f"{n} must be a contiguous CUDA float32 tensor"
+                                 + (f" of shape {shp}" if shp else ""))
+        if not 0 <= generation < erank_history.numel():
+            raise ValueError(f"generation {generation} is outside erank_history")
+        st = _lib.MultiHeadCAState(mass_buffer.data_ptr() if mass_buffer is not None else None,
+                                   ca_input.data_ptr(), ca_output.data_ptr())
+        _lib.check(self.lib.slime_neural_ca_update(self._h, ctypes.byref(st), _ptr(conc),
+                                                   _ptr(erank_history), int(generation),
+                                                   _stream(stream)))
+
     def field_from_state(self, x, stream=None):
         torch = _torch()
         conc = torch.empty((self.G, self.G), dtype=torch.float32, device="cuda")

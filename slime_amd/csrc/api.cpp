@@ -50,9 +50,10 @@ struct slime_ca {
 
     int fit_chunks = 0;
     int fit_T = 0;             // history length the fitness partials are sized for
-    float* gram_part = nullptr;
-    float* mom_part = nullptr;
+    double* gram_part = nullptr;
+    double* mom_part = nullptr;
     int* sweeps = nullptr;     // [B*H]
+    float* org_fit = nullptr;  // [3][B*H] erank, coherence, fitness of slime_neural_ca_update
 
     // Optional per-kernel timing: event pairs recorded around launches.
     bool timing = false;
@@ -152,7 +153,7 @@ void release(slime_ca* h) {
     h->ev_pool.clear();
     void* ptrs[] = {h->Wtm, h->Wt, h->K, h->mu, h->sigma, h->M, h->P, h->I, h->V, h->S[0], h->S[1], h->Sf,
                     h->part_in, h->part_out, h->scale[0], h->scale[1], h->unit_scale,
-                    h->mass_in, h->mass_out, h->gram_part, h->mom_part, h->sweeps};
+                    h->mass_in, h->mass_out, h->gram_part, h->mom_part, h->sweeps, h->org_fit};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
 }
@@ -246,6 +247,48 @@ int run_stencil(slime_ca* h, const void* x, const float* x_scale, const void* P,
     HIP_TRY(timed(h, h->stencil_ev, s, [&] { return launch_stencil(c.dtype, a, s); }));
     HIP_TRY(launch_mass_finalize(h->part_in, h->part_out, c.B * c.H, h->tiles, h->mass_in,
                                  h->mass_out, out_scale, s));
+    return SLIME_OK;
+}
+
+
+// E1-E5 over T states, state t at x_hist + t * t_stride bytes.
+int run_fitness(slime_ca* h, const void* x_hist, long long t_stride, int T, float* erank,
+                float* coherence, float* fitness, hipStream_t s) {
+    const slime_ca_config& c = h->cfg;
+    const size_t BH = (size_t)c.B * c.H;
+    const int chunks = fitness_chunks(c.G);
+    if (chunks < 1) return fail(SLIME_EINVAL, "grid too small for the fitness pass");
+    int rc = SLIME_OK;
+    if (!h->gram_part || h->fit_chunks != chunks) {
+        if (h->gram_part) (void)hipFree(h->gram_part);
+        h->gram_part = nullptr;
+        rc = dalloc_t(&h->gram_part, BH * chunks * c.D * c.D * 8);
+        if (rc) return rc;
+        h->fit_chunks = chunks;
+    }
+    if (!h->mom_part || h->fit_T < T) {
+        if (h->mom_part) (void)hipFree(h->mom_part);
+        h->mom_part = nullptr;
+        rc = dalloc_t(&h->mom_part, BH * chunks * (size_t)(T - 1) * 5 * 8);
+        if (rc) return rc;
+        h->fit_T = T;
+    }
+    h->last_stream = s;
+    FitnessArgs f{};
+    f.hist = x_hist;
+    f.t_stride = t_stride;
+    f.T = T;
+    f.B = c.B;
+    f.G = c.G;
+    f.D = c.D;
+    f.gram_part = h->gram_part;
+    f.mom_part = h->mom_part;
+    f.chunks = chunks;
+    f.erank = erank;
+    f.coh = coherence;
+    f.fitness = fitness;
+    f.sweeps = h->sweeps;
+    HIP_TRY(launch_fitness(c.dtype, f, s));
     return SLIME_OK;
 }
 
@@ -451,41 +494,8 @@ int slime_ca_fitness(slime_ca* h, const void* x_hist, int T, float* erank, float
     if (!x_hist || !erank || !coherence || !fitness)
         return fail(SLIME_EINVAL, "a tensor pointer is NULL");
     if (T < 2 || T > 65) return fail(SLIME_EINVAL, "T=%d must be in [2, 65]", T);
-    const slime_ca_config& c = h->cfg;
-    const size_t BH = (size_t)c.B * c.H;
-    const int chunks = fitness_chunks(c.G);
-    if (chunks < 1) return fail(SLIME_EINVAL, "grid too small for the fitness pass");
-    if (!h->gram_part || h->fit_chunks != chunks) {
-        if (h->gram_part) (void)hipFree(h->gram_part);
-        h->gram_part = nullptr;
-        rc = dalloc_t(&h->gram_part, BH * chunks * c.D * c.D * 4);
-        if (rc) return rc;
-        h->fit_chunks = chunks;
-    }
-    if (!h->mom_part || h->fit_T < T) {
-        if (h->mom_part) (void)hipFree(h->mom_part);
-        h->mom_part = nullptr;
-        rc = dalloc_t(&h->mom_part, BH * chunks * (size_t)(T - 1) * 5 * 4);
-        if (rc) return rc;
-        h->fit_T = T;
-    }
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    h->last_stream = s;
-    FitnessArgs f{};
-    f.hist = x_hist;
-    f.T = T;
-    f.B = c.B;
-    f.G = c.G;
-    f.D = c.D;
-    f.gram_part = h->gram_part;
-    f.mom_part = h->mom_part;
-    f.chunks = chunks;
-    f.erank = erank;
-    f.coh = coherence;
-    f.fitness = fitness;
-    f.sweeps = h->sweeps;
-    HIP_TRY(launch_fitness(c.dtype, f, s));
-    return SLIME_OK;
+    return run_fitness(h, x_hist, h->state_elems * (long long)h->elem, T, erank, coherence,
+                       fitness, static_cast<hipStream_t>(stream));
 }
 
 int slime_ca_fitness_sweeps(slime_ca* h, int* h_sweeps) {
@@ -515,6 +525,40 @@ int slime_ca_field_from_state(slime_ca* h, const void* x, float* conc, void* str
     hipStream_t s = static_cast<hipStream_t>(stream);
     h->last_stream = s;
     HIP_TRY(launch_field_from_state(h->cfg.dtype, x, conc, h->cfg.G, h->C, s));
+    return SLIME_OK;
+}
+
+int slime_neural_ca_update(slime_ca* h, const slime_multihead_ca_state* st, float* conc,
+                           float* erank_hist, int generation, void* stream) {
+    int rc = use_handle(h);
+    if (rc) return rc;
+    if (!h->params_set) return fail(SLIME_ESTATE, "slime_ca_set_params has not been called");
+    if (!st || !st->ca_input || !st->ca_output || !conc || !erank_hist)
+        return fail(SLIME_EINVAL, "a tensor pointer is NULL");
+    if (st->ca_input == st->ca_output)
+        return fail(SLIME_EINVAL, "ca_input and ca_output must be distinct buffers");
+    if (h->cfg.B != 1) return fail(SLIME_EINVAL, "the organism update needs a handle with B=1");
+    if (generation < 0) return fail(SLIME_EINVAL, "generation=%d is negative", generation);
+    const long long t_stride =
+        static_cast<const char*>(st->ca_output) - static_cast<const char*>(st->ca_input);
+    if (t_stride % (long long)h->elem)
+        return fail(SLIME_EINVAL, "ca_input and ca_output are not element-aligned to each other");
+    const size_t BH = (size_t)h->cfg.B * h->cfg.H;
+    if (!h->org_fit) {
+        rc = dalloc_t(&h->org_fit, 3 * BH * 4);
+        if (rc) return rc;
+    }
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    h->last_stream = s;
+    HIP_TRY(launch_init_from_field(h->cfg.dtype, conc, st->ca_input, h->cfg.G, h->C, s));
+    rc = slime_ca_step(h, st->ca_input, st->ca_output, 1, stream);
+    if (rc) return rc;
+    HIP_TRY(launch_field_from_state(h->cfg.dtype, st->ca_output, conc, h->cfg.G, h->C, s));
+    rc = run_fitness(h, st->ca_input, t_stride, 2, h->org_fit, h->org_fit + BH,
+                     h->org_fit + 2 * BH, s);
+    if (rc) return rc;
+    HIP_TRY(launch_organism_report(h->mass_out, h->org_fit, h->cfg.H, st->mass_buffer,
+                                   erank_hist + generation, s));
     return SLIME_OK;
 }
 

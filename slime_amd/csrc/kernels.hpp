@@ -70,10 +70,11 @@ hipError_t launch_rescale(int dtype, const void* x, int x_f32, const float* scal
 
 // ---- E1-E5 fitness --------------------------------------------------------------------
 struct FitnessArgs {
-    const void* hist;   // [T][B][G][G][C]
+    const void* hist;   // state 0 of the history, each state [B][G][G][C]
+    long long t_stride; // bytes from state t to state t + 1 (may be negative)
     int T, B, G, D;
-    float* gram_part;   // [B*H][chunks][D*D]
-    float* mom_part;    // [B*H][chunks][(T-1)*5]
+    double* gram_part;  // [B*H][chunks][D*D]
+    double* mom_part;   // [B*H][chunks][(T-1)*5]
     int chunks;
     float* erank;       // [B][H]
     float* coh;
@@ -88,5 +89,7 @@ hipError_t launch_init_from_field(int dtype, const float* conc, void* X, int G, 
                                   hipStream_t s);
 hipError_t launch_field_from_state(int dtype, const void* X, float* conc, int G, int C,
                                    hipStream_t s);
+hipError_t launch_organism_report(const double* mass_out, const float* erank, int H,
+                                  float* mass_buffer, float* erank_out, hipStream_t s);
 
 }  // namespace slime

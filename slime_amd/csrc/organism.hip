@@ -6,6 +6,9 @@
 //   update_field_from_ca_kernel      conc[y,x] = mean_c X[y,x,c]
 //                                    slime/core/organism.cu:723-743
 // One wave per cell for the field update (a wave64 DPP sum over the channels).
+// organism_report_kernel writes what neural_ca_update_kernel
+// (slime/core/organism.cu:617-688) leaves behind per generation: the per-head mass
+// buffer and one effective-rank entry of the history.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -33,7 +36,29 @@ __global__ __launch_bounds__(256) void field_from_state_kernel(const T* X, float
     if (valid && lane == 0) conc[cell] = s / (float)C;
 }
 
+// After one organism generation: mass_buffer[h] = conserved mass of head h (may be
+// null) and *erank_out = mean over heads of the effective rank, added in head order.
+__global__ __launch_bounds__(64) void organism_report_kernel(const double* mass_out,
+                                                             const float* erank, int H,
+                                                             float* mass_buffer,
+                                                             float* erank_out) {
+    const int h = threadIdx.x;
+    if (mass_buffer && h < H) mass_buffer[h] = (float)mass_out[h];
+    if (h == 0) {
+        float s = 0.f;
+        for (int i = 0; i < H; ++i) s += erank[i];
+        *erank_out = s / (float)H;
+    }
+}
+
 }  // namespace
+
+hipError_t launch_organism_report(const double* mass_out, const float* erank, int H,
+                                  float* mass_buffer, float* erank_out, hipStream_t s) {
+    hipLaunchKernelGGL(organism_report_kernel, dim3(1), dim3(64), 0, s, mass_out, erank, H,
+                       mass_buffer, erank_out);
+    return hipGetLastError();
+}
 
 hipError_t launch_init_from_field(int dtype, const float* conc, void* X, int G, int C, hipStream_t s) {
     const long long total = (long long)G * G * C;

@@ -16,7 +16,7 @@ def _header_functions():
     with open(os.path.join(ROOT, "include", "slime_ca.h")) as f:
         text = f.read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(slime_ca_\w+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(slime_(?:ca|neural_ca)_\w+)\s*\(", text)))
 
 
 def test_header_declares_the_exported_set():
@@ -57,6 +57,7 @@ def test_null_arguments_are_errors_not_crashes():
     assert lib.slime_ca_set_params(None, None) == _lib.SLIME_EINVAL
     assert lib.slime_ca_destroy(None) == _lib.SLIME_OK
     assert lib.slime_ca_uses_mfma(None) == 0
+    assert lib.slime_neural_ca_update(None, None, None, None, 0, None) == _lib.SLIME_EINVAL
     assert b"NULL" in lib.slime_ca_last_error()
 
 
