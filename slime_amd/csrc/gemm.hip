@@ -9,16 +9,19 @@
 // Tile: 256 cells x 256 outputs per 256-thread workgroup (4 waves, each 128x128
 // as 4x4 MFMA 32x32 blocks), one persistent workgroup per CU. K advances in
 // 64-byte slabs (32 bf16 / 16 fp32) through a 4-stage LDS ring filled by direct
-// global->LDS loads (global_load_lds_dwordx4), three slabs ahead of the MFMAs, so
-// each slab's load latency hides behind three slabs of MFMA work. The four
-// stages are separate LDS arrays: the compiler then knows that reading one stage
-// does not wait for the loads still landing in the others. 16-byte chunks are
-// XOR-swizzled by row pair, so the DMA writes and the operand reads avoid bank
-// conflicts. The weights are the MFMA "A" operand: a lane's accumulators hold 4
-// consecutive output channels of one cell. The bf16 epilogue goes through LDS
-// so that stores leave as whole 128-byte row segments. Workgroups walk an
-// XCD-contiguous tile range, N fastest, so a cell block and one batch's weights
-// are re-read from that XCD's L2.
+// global->LDS loads (global_load_lds_dwordx4), so three slabs are in flight while
+// one is consumed. Operand fragments are double-buffered in registers: while a
+// wave issues the 32 MFMAs of slab k from one buffer, it reads slab k+1's
+// fragments into the other and issues the loads of slab k+4, so the matrix cores
+// never wait for an LDS round trip; one barrier per slab publishes slab k+1 and
+// frees the stage of slab k. Stages are laid out in fragment order (each MFMA
+// operand read is one linear 1 KiB block: no bank conflicts). The first MFMA of
+// a tile starts from a zero accumulator instead of clearing 256 registers. The
+// weights are the MFMA "A" operand: a lane's accumulators hold 4 consecutive
+// output channels of one cell. The bf16 epilogue goes through LDS so that stores
+// leave as whole 128-byte row segments. Workgroups walk an XCD-contiguous tile
+// range, N fastest, so a cell block and one batch's weights are re-read from that
+// XCD's L2.
 #include <type_traits>
 
 #include "common.hpp"
@@ -28,23 +31,18 @@ namespace slime {
 namespace {
 
 
-template <int R0, int N, typename F>
-__device__ __forceinline__ void static_for_gemm(F&& f) {
-    if constexpr (R0 < N) {
-        f(std::integral_constant<int, R0>{});
-        static_for_gemm<R0 + 1, N>(f);
-    }
-}
-
 constexpr int kBM = 256, kBN = 256, kThreads = 256;
 constexpr int kSlabB = 64;                    // bytes of K per tile row per slab
 constexpr int kStageB = (kBM + kBN) * kSlabB;  // 32 KiB
-constexpr int kAhead = 3;                     // slabs in flight ahead of the MFMAs
+constexpr int kDmaPerSlab = 8;                // direct-load instructions per wave per slab
 
-// Byte offset of 16-byte chunk c (0..3) of tile row r inside a stage.
-__device__ __forceinline__ int swz(int row, int chunk) {
-    return row * kSlabB + ((chunk ^ ((row >> 1) & 3)) << 4);
-}
+// Stage layout: tile row r (0..255 cells, 256..511 output channels) holds its 64
+// slab bytes at r*64, as four 16-byte chunks XOR-permuted by
+// f(r) = ((r >> 1) ^ (r >> 3)) & 3: physical chunk = logical chunk ^ f(r). One
+// direct-load instruction fills 16 whole rows (1 KiB, four lanes per 64-byte row),
+// and the operand reads -- 32 consecutive rows at one logical chunk per half
+// wave -- spread over the LDS banks.
+__device__ __forceinline__ constexpr int row_swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
 
 __device__ __forceinline__ float apply_act(float v, int act) {
     if (act == 1) return v > 0.f ? v : 0.f;
@@ -137,38 +135,25 @@ __device__ __forceinline__ unsigned lds_addr(const void* p) {
     return (unsigned)(size_t)(const lds_void_t*)p;
 }
 
-// Issues the direct global->LDS loads of slab ks of a tile into one stage. A wave
-// instruction fills 1 KiB of LDS = 16 tile rows of 64 bytes: lane l lands at row
-// R + l/4, physical chunk l%4, so it fetches logical chunk (l%4) ^ ((l/8)%4) of
-// that row. Wave w issues row groups (4j + w)*16, j = 0..7: A rows, then Bt rows.
-template <typename T>
-__device__ __forceinline__ void issue_slab(const GemmArgs& g, int tile, int nN, int ks, int wave,
-                                           int lane, unsigned char* stage) {
-    constexpr int kE = 16 / (int)sizeof(T);
-    constexpr int kSlabE = kSlabB / (int)sizeof(T);
-    const int m0 = (tile / nN) * kBM, n0 = (tile % nN) * kBN;
-    const long long K = g.K;
-    const char* a = reinterpret_cast<const char*>(static_cast<const T*>(g.A) + m0 * K + ks * kSlabE);
-    const char* b = reinterpret_cast<const char*>(
-        static_cast<const T*>(g.Bt) + (long long)(m0 / g.rows_per_batch) * g.bt_batch_stride + n0 * K +
-        ks * kSlabE);
-    const int sub = lane >> 2;
-    const int chunk = (lane & 3) ^ ((lane >> 3) & 3);
-    const unsigned lane_off = (unsigned)((sub * K + chunk * kE) * (long long)sizeof(T));
-    const unsigned row_bytes = (unsigned)(K * sizeof(T));
-    const unsigned sbase = lds_addr(stage);
+// Issues the direct global->LDS loads of slab ks of a tile into the stage at LDS
+// byte address sbase: 32 instructions of 16 rows each; wave w issues row groups
+// w, w+4, ..., w+28 (16 cell groups, then 16 weight groups). x, w: the tile's
+// first cell row and first weight row plus this lane's offset (row lane/4 of the
+// group, the logical chunk that lands in physical chunk lane%4).
+__device__ __forceinline__ void issue_slab(const char* x, const char* w, long long row_bytes, int ks,
+                                           int wave, unsigned sbase) {
+    const long long k_off = (long long)ks * kSlabB;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const int R = (4 * j + wave) * 16;
-        dma16(a + R * row_bytes + lane_off, sbase + R * kSlabB);
+        const int grp = 4 * j + wave;
+        dma16(x + grp * 16 * row_bytes + k_off, sbase + grp * 1024);
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const int R = (4 * j + wave) * 16;
-        dma16(b + R * row_bytes + lane_off, sbase + (kBM + R) * kSlabB);
+        const int grp = 4 * j + wave;
+        dma16(w + grp * 16 * row_bytes + k_off, sbase + (16 + grp) * 1024);
     }
 }
-constexpr int kDmaPerSlab = 8;  // DMA instructions per wave per slab
 
 // s_waitcnt vmcnt(n) for the counts the pipeline needs (immediate operand).
 __device__ __forceinline__ void wait_vm(int n) {
@@ -178,6 +163,7 @@ __device__ __forceinline__ void wait_vm(int n) {
         case 0: __builtin_amdgcn_s_waitcnt(SLIME_VMCNT(0)); break;
         case 8: __builtin_amdgcn_s_waitcnt(SLIME_VMCNT(8)); break;
         case 16: __builtin_amdgcn_s_waitcnt(SLIME_VMCNT(16)); break;
+        case 24: __builtin_amdgcn_s_waitcnt(SLIME_VMCNT(24)); break;
         case 32: __builtin_amdgcn_s_waitcnt(SLIME_VMCNT(32)); break;
         case 40: __builtin_amdgcn_s_waitcnt(SLIME_VMCNT(40)); break;
         case 48: __builtin_amdgcn_s_waitcnt(SLIME_VMCNT(48)); break;
@@ -186,10 +172,6 @@ __device__ __forceinline__ void wait_vm(int n) {
 #undef SLIME_VMCNT
 }
 
-// Persistent: each workgroup walks tiles tile0, tile0 + stride, ... of its XCD's
-// contiguous range. Slab s of every tile lives in stage s % 4; slabs of the next
-// tile are fetched while the current tile finishes, so tiles follow each other
-// with only the epilogue in between.
 // Workgroup barrier for LDS data only: __syncthreads() would also wait for every
 // outstanding vector-memory operation (its release fence covers the direct loads
 // of later slabs and the previous tile's stores), draining the pipeline.
@@ -200,15 +182,124 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("" ::: "memory");
 }
 
+// Operand fragments of one slab for one wave: weights (A operand, 4 blocks of 32
+// output channels) and cells (B operand, 4 blocks of 32 cells), per 32-byte half kk.
+struct Frags {
+    u32x4 w[2][4];
+    u32x4 x[2][4];
+};
+
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<I + 1, N>(f);
+    }
+}
+
+// Per-lane LDS byte offsets of this wave's fragments inside a stage, per half kk:
+// x = its first cell row block, w = its first weight row block (row lane%32,
+// physical chunk of logical chunk 2*kk + lane/32).
+struct FragBase {
+    unsigned x[2], w[2];
+};
+
+// Fragment read R (0..15) of the slab in the stage at `stage`, in the order the
+// MFMAs consume them: per half kk, the 4 cell blocks then the 4 weight blocks
+// (block q = 32 rows further).
+template <int R>
+__device__ __forceinline__ void read_frag(Frags& f, const unsigned char* stage, const FragBase& b) {
+    constexpr int kk = R >> 3, q = R & 7;
+    if constexpr (q < 4)
+        f.x[kk][q] = *reinterpret_cast<const u32x4*>(stage + b.x[kk] + q * 32 * kSlabB);
+    else
+        f.w[kk][q - 4] = *reinterpret_cast<const u32x4*>(stage + b.w[kk] + (q - 4) * 32 * kSlabB);
+}
+
+// MFMA group M (0..31) of a slab: output block (i, j) = ((M / 4) % 4, M % 4) over
+// half kk = M / 16; one bf16 MFMA or four fp32 MFMAs. kZero: start from 0.
+template <typename T, bool kZero, int M>
+__device__ __forceinline__ void mfma_group(f32x16 (&acc)[4][4], const Frags& f) {
+    constexpr int kk = M >> 4, i = (M >> 2) & 3, j = M & 3;
+    f32x16 c = acc[i][j];
+    if constexpr (kZero) c = f32x16{};
+    if constexpr (sizeof(T) == 2) {
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_v, f.w[kk][i]),
+                                                            __builtin_bit_cast(bf16x8_v, f.x[kk][j]), c,
+                                                            0, 0, 0);
+    } else {
+        const f32x4 wv = __builtin_bit_cast(f32x4, f.w[kk][i]);
+        const f32x4 xv = __builtin_bit_cast(f32x4, f.x[kk][j]);
+        f32x16 a = __builtin_amdgcn_mfma_f32_32x32x2f32(wv[0], xv[0], c, 0, 0, 0);
+        a = __builtin_amdgcn_mfma_f32_32x32x2f32(wv[1], xv[1], a, 0, 0, 0);
+        a = __builtin_amdgcn_mfma_f32_32x32x2f32(wv[2], xv[2], a, 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(wv[3], xv[3], a, 0, 0, 0);
+    }
+}
+
+// The tile/slab schedule a workgroup follows: persistent, each workgroup walks
+// tiles tile, tile + stride, ... below tile_end (an XCD-contiguous range).
+struct Walk {
+    int tile, next, stride, tile_end, nN, nk;
+    long long row_bytes;
+    const char *x_cur, *w_cur;  // this tile's operand rows (+ lane offset)
+    const char *x_nxt, *w_nxt;  // the next tile's, or this tile's when it is the last
+};
+
+// Operand row pointers of a tile, with the lane's offset folded in.
+template <typename T>
+__device__ __forceinline__ void tile_rows(const GemmArgs& g, int tile, int nN, long long lane_off,
+                                          const char** x, const char** w) {
+    const int m0 = (tile / nN) * kBM, n0 = (tile % nN) * kBN;
+    const long long K = g.K;
+    *x = reinterpret_cast<const char*>(static_cast<const T*>(g.A) + m0 * K) + lane_off;
+    *w = reinterpret_cast<const char*>(static_cast<const T*>(g.Bt) +
+                                       (long long)(m0 / g.rows_per_batch) * g.bt_batch_stride + n0 * K) +
+         lane_off;
+}
+
+// Scheduling-group masks (LLVM AMDGPU IGroupLP): MFMA and LDS-read instructions.
+constexpr int kSchedMfma = 0x008, kSchedDsRead = 0x100;
+
+// One slab step: slab kt of the current tile sits in stage S and its fragments in
+// `cur`. Waits for slab kt+1, issues the 8 direct loads of slab kt+4 into stage S
+// and the 16 fragment reads of slab kt+1 (stage (S+1)%4, into `nxt`) interleaved
+// with the first 8 of the 32 MFMA groups of slab kt, then the other 24: the
+// reads land while the matrix cores work, and nothing waits for LDS inside the
+// step. Past the last slab of the last tile the reads pick up stale stage data
+// and the loads refetch a valid slab, so every step issues the same instructions
+// and the vmcnt bookkeeping stays uniform.
+template <typename T, int S, bool kFirstSlab>
+__device__ __forceinline__ void slab_step(const Walk& wk, int kt, int wave, unsigned char* lds,
+                                          const FragBase& fb, f32x16 (&acc)[4][4], const Frags& cur,
+                                          Frags& nxt, int younger) {
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vm(younger);
+    lds_barrier();  // slab kt+1 is in LDS; every wave is done reading stage S
+    const int ks = kt + 4;
+    const bool same = ks < wk.nk;
+    issue_slab(same ? wk.x_cur : wk.x_nxt, same ? wk.w_cur : wk.w_nxt, wk.row_bytes,
+               same ? ks : ks - wk.nk, wave, lds_addr(lds + S * kStageB));
+    const unsigned char* rd = lds + ((S + 1) & 3) * kStageB;
+    static_for<0, 16>([&](auto r) { read_frag<decltype(r)::value>(nxt, rd, fb); });
+    static_for<0, 32>([&](auto m) {
+        constexpr int M = decltype(m)::value;
+        mfma_group<T, kFirstSlab && M < 16, M>(acc, cur);
+    });
+    static_for<0, 8>([&](auto) {
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, sizeof(T) == 2 ? 1 : 4, 0);
+    });
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, sizeof(T) == 2 ? 24 : 96, 0);
+    __builtin_amdgcn_sched_barrier(0);
+}
+
 template <typename T>
 __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs g) {
-    __shared__ __attribute__((aligned(16))) unsigned char st0[kStageB];
-    __shared__ __attribute__((aligned(16))) unsigned char st1[kStageB];
-    __shared__ __attribute__((aligned(16))) unsigned char st2[kStageB];
-    __shared__ __attribute__((aligned(16))) unsigned char st3[kStageB];
-    constexpr int kSlabE = kSlabB / (int)sizeof(T);
+    __shared__ __attribute__((aligned(1024))) unsigned char lds[4 * kStageB];
     constexpr bool kBf16 = sizeof(T) == 2;
     constexpr int kStores = kBf16 ? kStoresBf16 : kStoresF32;
+    constexpr int kSlabE = kSlabB / (int)sizeof(T);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -216,107 +307,78 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs g) {
     const int wm = wave & 1, wn = wave >> 1;
     const int r32 = lane & 31, half = lane >> 5;
 
-    const int nN = g.N / kBN;
-    const int ntiles = (g.M / kBM) * nN;
-    const int nk = g.K / kSlabE;  // slabs per tile, a multiple of 4
-    int tile, stride, tile_end;
+    Walk wk;
+    wk.nN = g.N / kBN;
+    wk.nk = g.K / kSlabE;  // slabs per tile, a multiple of 4
+    wk.row_bytes = (long long)g.K * (long long)sizeof(T);
+    // Direct loads: lane l fills physical chunk l%4 of row l/4 of a 16-row group whose
+    // first row is a multiple of 32 for even waves and 16 more for odd ones.
+    const int dma_row = lane >> 2;
+    const int dma_chunk = (lane & 3) ^ row_swz(16 * (wave & 1) + dma_row);
+    const long long lane_off = dma_row * wk.row_bytes + dma_chunk * 16;
+    const int ntiles = (g.M / kBM) * wk.nN;
     if ((gridDim.x & 7) == 0) {
         const int per_xcd_wg = gridDim.x >> 3;
         const int xcd = blockIdx.x & 7, j = blockIdx.x >> 3;
         const int span = (ntiles + 7) >> 3;
         const int begin = xcd * span;
-        tile_end = min(ntiles, begin + span);
-        tile = begin + j;
-        stride = per_xcd_wg;
+        wk.tile_end = min(ntiles, begin + span);
+        wk.tile = begin + j;
+        wk.stride = per_xcd_wg;
     } else {
-        tile = blockIdx.x;
-        stride = gridDim.x;
-        tile_end = ntiles;
+        wk.tile = blockIdx.x;
+        wk.stride = gridDim.x;
+        wk.tile_end = ntiles;
     }
-    if (tile >= tile_end) return;
+    if (wk.tile >= wk.tile_end) return;
 
-    auto stage_ptr = [&](int s) -> unsigned char* {
-        return s == 0 ? st0 : s == 1 ? st1 : s == 2 ? st2 : st3;
-    };
-    // Prologue: the first kAhead slabs of the first tile.
-    for (int s = 0; s < kAhead; ++s) issue_slab<T>(g, tile, nN, s, wave, lane, stage_ptr(s));
-    bool stores_pending = false;  // the previous tile's epilogue stores follow slabs 0..2
+    FragBase fbase;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+        const unsigned lane_part = r32 * kSlabB + (((2 * kk + half) ^ row_swz(r32)) << 4);
+        fbase.x[kk] = lane_part + (wm * 128) * kSlabB;
+        fbase.w[kk] = lane_part + (kBM + wn * 128) * kSlabB;
+    }
 
+    // Prologue: slabs 0..3 of the first tile, then slab 0's fragments.
+    tile_rows<T>(g, wk.tile, wk.nN, lane_off, &wk.x_cur, &wk.w_cur);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) issue_slab(wk.x_cur, wk.w_cur, wk.row_bytes, s, wave, lds_addr(lds + s * kStageB));
+    wait_vm(3 * kDmaPerSlab);
+    lds_barrier();
+    Frags fa, fb;
+    static_for<0, 16>([&](auto r) { read_frag<decltype(r)::value>(fa, lds, fbase); });
+
+    bool stores_pending = false;  // the previous tile's stores follow slabs 0..3 of this one
     f32x16 acc[4][4];
     while (true) {
-        const int next = tile + stride < tile_end ? tile + stride : -1;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-                for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
-
-        for (int kb = 0; kb < nk; kb += 4) {
-            static_for_gemm<0, 4>([&](auto sc) {
-                constexpr int S = decltype(sc)::value;
-                unsigned char* cur = S == 0 ? st0 : S == 1 ? st1 : S == 2 ? st2 : st3;
-                unsigned char* fill = S == 0 ? st3 : S == 1 ? st0 : S == 2 ? st1 : st2;  // (S+3)%4
-                const int kt = kb + S;
-                // This wave's loads of slab kt have landed once only the younger
-                // ones remain outstanding: slabs kt+1, kt+2 (when they exist) and,
-                // for the first three slabs after an epilogue, its stores.
-                const bool has1 = kt + 1 < nk || next >= 0;
-                const bool has2 = kt + 2 < nk || next >= 0;
-                int younger = (has1 ? kDmaPerSlab : 0) + (has2 ? kDmaPerSlab : 0);
-                if (stores_pending && kt < kAhead) younger = kStores <= 32 ? younger + kStores : 0;
-                wait_vm(younger);
-                lds_barrier();  // every wave's part of slab kt is in LDS; slab kt-1 is consumed
-                // Refill the stage of slab kt-1 with slab kt+3 (this tile or the next).
-                if (kt + kAhead < nk)
-                    issue_slab<T>(g, tile, nN, kt + kAhead, wave, lane, fill);
-                else if (next >= 0)
-                    issue_slab<T>(g, next, nN, kt + kAhead - nk, wave, lane, fill);
-                if (kt + 1 >= kAhead) stores_pending = false;
-                uint4 wf[2][4], xf[2][4];
-#pragma unroll
-                for (int kk = 0; kk < 2; ++kk) {
-                    const int chunk = 2 * kk + half;
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        wf[kk][i] = *reinterpret_cast<const uint4*>(cur + swz(kBM + wn * 128 + i * 32 + r32, chunk));
-#pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        xf[kk][j] = *reinterpret_cast<const uint4*>(cur + swz(wm * 128 + j * 32 + r32, chunk));
-                }
-#pragma unroll
-                for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-#pragma unroll
-                        for (int j = 0; j < 4; ++j) {
-                            if constexpr (kBf16) {
-                                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                                    __builtin_bit_cast(bf16x8_v, wf[kk][i]),
-                                    __builtin_bit_cast(bf16x8_v, xf[kk][j]), acc[i][j], 0, 0, 0);
-                            } else {
-                                const f32x4 wv = __builtin_bit_cast(f32x4, wf[kk][i]);
-                                const f32x4 xv = __builtin_bit_cast(f32x4, xf[kk][j]);
-#pragma unroll
-                                for (int s = 0; s < 4; ++s)
-                                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(wv[s], xv[s],
-                                                                                     acc[i][j], 0, 0, 0);
-                            }
-                        }
-            });
+        wk.next = wk.tile + wk.stride < wk.tile_end ? wk.tile + wk.stride : -1;
+        if (wk.next >= 0) tile_rows<T>(g, wk.next, wk.nN, lane_off, &wk.x_nxt, &wk.w_nxt);
+        else wk.x_nxt = wk.x_cur, wk.w_nxt = wk.w_cur;
+        // Loads younger than slab kt+1 when step kt waits for it: slabs kt+2 and
+        // kt+3, and for kt <= 2 after an epilogue also that epilogue's stores.
+        constexpr int y_store = kStores + 2 * kDmaPerSlab <= 63 ? kStores + 2 * kDmaPerSlab : 0;
+        const int y_first = stores_pending ? y_store : 2 * kDmaPerSlab;
+        slab_step<T, 0, true>(wk, 0, wave, lds, fbase, acc, fa, fb, y_first);
+        slab_step<T, 1, false>(wk, 1, wave, lds, fbase, acc, fb, fa, y_first);
+        slab_step<T, 2, false>(wk, 2, wave, lds, fbase, acc, fa, fb, y_first);
+        slab_step<T, 3, false>(wk, 3, wave, lds, fbase, acc, fb, fa, 2 * kDmaPerSlab);
+        for (int kb = 4; kb < wk.nk; kb += 4) {
+            slab_step<T, 0, false>(wk, kb + 0, wave, lds, fbase, acc, fa, fb, 2 * kDmaPerSlab);
+            slab_step<T, 1, false>(wk, kb + 1, wave, lds, fbase, acc, fb, fa, 2 * kDmaPerSlab);
+            slab_step<T, 2, false>(wk, kb + 2, wave, lds, fbase, acc, fa, fb, 2 * kDmaPerSlab);
+            slab_step<T, 3, false>(wk, kb + 3, wave, lds, fbase, acc, fb, fa, 2 * kDmaPerSlab);
         }
-
-        // Epilogue: the whole 256-wide N tile lies in one output plane, so the
-        // activation is uniform over the tile.
-        const int m0 = (tile / nN) * kBM, n0 = (tile % nN) * kBN;
+        // fa now holds slab 0 of the next tile (stage 0). Stage 0 becomes the
+        // epilogue's staging area once every wave has read it.
+        const int m0 = (wk.tile / wk.nN) * kBM, n0 = (wk.tile % wk.nN) * kBN;
         const int plane = n0 / g.ncol;
         T* out = static_cast<T*>(g.out[plane]);
         const int col0 = n0 - plane * g.ncol + wn * 128;
+        // The whole 256-wide N tile lies in one output plane: uniform activation.
         if constexpr (kBf16) {
-            // The last slab's stage (3) is free once every wave has read it; the
-            // other three are receiving the next tile's first slabs.
             lds_barrier();
-            unsigned char* ep = st3 + wave * kEpiWaveB;
+            unsigned char* ep = lds + wave * kEpiWaveB;
             bf16_t* obase = reinterpret_cast<bf16_t*>(out) + (long long)(m0 + wm * 128) * g.ncol + col0;
             switch (g.act[plane]) {
                 case 1: store_tile_bf16<1>(acc, obase, g.ncol, ep, lane); break;
@@ -333,9 +395,13 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs g) {
             }
         }
         stores_pending = true;
-        if (next < 0) break;
-        tile = next;
+        if (wk.next < 0) break;
+        wk.tile = wk.next;
+        wk.x_cur = wk.x_nxt;
+        wk.w_cur = wk.w_nxt;
     }
+    // Loads refetched past the last slab may still be landing in LDS.
+    wait_vm(0);
 }
 
 // Any-shape fallback: one thread per output, fp32 accumulation.
