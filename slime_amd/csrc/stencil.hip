@@ -81,6 +81,25 @@ __device__ __forceinline__ void wait_vm0() {
     __builtin_amdgcn_s_waitcnt(0x0F70);  // s_waitcnt vmcnt(0)
 }
 
+__device__ __forceinline__ unsigned lds_addr(const void* p) {
+    return (unsigned)(size_t)(const lds_void_t*)p;
+}
+
+// One direct global->LDS load (global_load_lds_dwordx4, SGPR base + 32-bit lane
+// offset): 16 bytes per lane from base + voff land at LDS byte address
+// lds + 16 * lane. Issued through inline asm so that the per-lane addresses stay
+// 32-bit (no 64-bit pointer per load held across the head loop); the kernel
+// waits for these loads itself (wait_vm0) before the barrier that publishes them.
+__device__ __forceinline__ void dma16_saddr(const void* base, unsigned voff, unsigned lds) {
+    asm volatile(
+        "s_mov_b32 m0, %0\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, %2"
+        :
+        : "s"(lds), "v"(voff), "s"(base)
+        : "memory", "m0");
+}
+
 // Workgroup barrier for LDS data only. __syncthreads() also waits for every
 // outstanding vector-memory operation (its release fence covers the direct
 // loads still landing in the other staging buffer); this waits for this wave's
@@ -134,6 +153,19 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+template <int kN>
+__device__ __forceinline__ float group_max(float v) {
+    if constexpr (kN >= 2) v = fmaxf(v, dpp_f32<0xB1>(v));
+    if constexpr (kN >= 4) v = fmaxf(v, dpp_f32<0x4E>(v));
+    if constexpr (kN >= 8) v = fmaxf(v, dpp_f32<0x141>(v));
+    return v;
+}
+
+// Score matrix of the MFMA score phase: 32 tile cells x 64 halo rows, fp32, rows
+// padded to 72 floats so the two half-waves of an MFMA result write (rows m and
+// m+4) land in different banks.
+constexpr int kScoreLd = 72;
+
 // TY: storage type of the unscaled output; fp32 when the caller rescales it into
 // the final bf16 state (one rounding instead of two).
 template <typename T, int D, typename TY>
@@ -147,6 +179,11 @@ __global__ __launch_bounds__((Layout<T, D>::kThreads), 2) void stencil_kernel(St
     __shared__ __attribute__((aligned(16))) unsigned char bufA[L::kBufB];
     __shared__ __attribute__((aligned(16))) unsigned char bufB[L::kBufB];
     __shared__ __attribute__((aligned(16))) float sAtt[2][kTileCells * kAStride];
+    // bf16, D = 64 (256 threads, 8 per cell): the scores <P, I> of all 32 cells
+    // against all 64 staged halo rows come from the matrix cores (v_mfma
+    // 32x32x16), 9 of each row are used.
+    constexpr bool kMfmaScores = sizeof(T) == 2 && D == 64;
+    __shared__ __attribute__((aligned(16))) float sS[kMfmaScores ? kTileCells * kScoreLd : 1];
     __shared__ __attribute__((aligned(16))) float sMS[H * kTileCells * 2];
     __shared__ float sR[L::kWaves * 16];
 
@@ -191,26 +228,31 @@ __global__ __launch_bounds__((Layout<T, D>::kThreads), 2) void stencil_kernel(St
                       (ch ^ (cell & L::kSwz)) * L::kCE;
         }
     }
-    const T* srcX = static_cast<const T*>(a.X) + bbase;
-    const T* srcV = static_cast<const T*>(a.V) + bbase;
-    const T* srcI = static_cast<const T*>(a.I) + bbase;
-    const T* srcP = static_cast<const T*>(a.P) + bbase;
+    const char* srcX = reinterpret_cast<const char*>(static_cast<const T*>(a.X) + bbase);
+    const char* srcV = reinterpret_cast<const char*>(static_cast<const T*>(a.V) + bbase);
+    const char* srcI = reinterpret_cast<const char*>(static_cast<const T*>(a.I) + bbase);
+    const char* srcP = reinterpret_cast<const char*>(static_cast<const T*>(a.P) + bbase);
+    // Byte offsets (within the batch entry) of this lane's 16-byte pieces.
+    unsigned boff_lin[L::kIA], boff_swz[L::kIA], boff_p[L::kPA];
+#pragma unroll
+    for (int k = 0; k < L::kIA; ++k) {
+        boff_lin[k] = (unsigned)hoff_lin[k] * (unsigned)sizeof(T);
+        boff_swz[k] = (unsigned)hoff_swz[k] * (unsigned)sizeof(T);
+    }
+#pragma unroll
+    for (int k = 0; k < L::kPA; ++k) boff_p[k] = (unsigned)poff[k] * (unsigned)sizeof(T);
     auto issue_head = [&](int h, unsigned char* buf) {
+        const unsigned hb = (unsigned)(h * D * (int)sizeof(T));
 #pragma unroll
         for (int k = 0; k < L::kIA; ++k) {
-            unsigned char* row = buf + (wave + k * L::kWaves) * 1024;
-            __builtin_amdgcn_global_load_lds((gbl_void_t*)(srcX + hoff_lin[k] + h * D),
-                                             (lds_void_t*)(row + L::offX), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds((gbl_void_t*)(srcV + hoff_lin[k] + h * D),
-                                             (lds_void_t*)(row + L::offV), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds((gbl_void_t*)(srcI + hoff_swz[k] + h * D),
-                                             (lds_void_t*)(row + L::offI), 16, 0, 0);
+            const unsigned row = lds_addr(buf) + (wave + k * L::kWaves) * 1024;
+            dma16_saddr(srcX, boff_lin[k] + hb, row + L::offX);
+            dma16_saddr(srcV, boff_lin[k] + hb, row + L::offV);
+            dma16_saddr(srcI, boff_swz[k] + hb, row + L::offI);
         }
 #pragma unroll
         for (int k = 0; k < L::kPA; ++k)
-            __builtin_amdgcn_global_load_lds((gbl_void_t*)(srcP + poff[k] + h * D),
-                                             (lds_void_t*)(buf + L::offP + (wave + k * L::kWaves) * 1024),
-                                             16, 0, 0);
+            dma16_saddr(srcP, boff_p[k] + hb, lds_addr(buf) + L::offP + (wave + k * L::kWaves) * 1024);
     };
 
     // Per-head parameters (and per-cell growth parameters) go to LDS once, before
@@ -277,7 +319,45 @@ __global__ __launch_bounds__((Layout<T, D>::kThreads), 2) void stencil_kernel(St
         if (h + 1 < H) issue_head(h + 1, nxt);
 
         // ---- phase A: attention scores (S4) and softmax --------------------------------
-        {
+        if constexpr (kMfmaScores) {
+            // Waves 0 and 1: S[cell][n] = <P_cell, I_n> for halo rows n of block 32*wave,
+            // K = D channels in steps of 16. A = P (row = cell), B = I^T (column = halo
+            // row); both operands are 16-byte chunks of swizzled rows.
+            if (wave < 2) {
+                const int m = lane & 31, kh = lane >> 5;
+                const int n = 32 * wave + m;
+                f32x16 acc = {};
+#pragma unroll
+                for (int ks = 0; ks < D / 16; ++ks) {
+                    const int c = 2 * ks + kh;
+                    const uint4 pa = *reinterpret_cast<const uint4*>(
+                        buf + L::offP + m * L::kRowB + ((c ^ (m & L::kSwz)) << 4));
+                    const uint4 ib = *reinterpret_cast<const uint4*>(
+                        buf + L::offI + n * L::kRowB + ((c ^ (n & L::kSwz)) << 4));
+                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_v, pa),
+                                                                  __builtin_bit_cast(bf16x8_v, ib), acc,
+                                                                  0, 0, 0);
+                }
+#pragma unroll
+                for (int e = 0; e < 16; ++e)
+                    sS[(8 * (e >> 2) + 4 * kh + (e & 3)) * kScoreLd + n] = acc[e];
+            }
+            lds_barrier();
+            // Softmax over the 9 neighbours: 8 lanes per cell, lane j takes neighbour j,
+            // lane 0 also neighbour 8.
+            const int cell = tid >> 3, j = tid & 7;
+            const int cy = cell / kTileX, cx = cell % kTileX;
+            const float* srow = sS + cell * kScoreLd;
+            const float sj = srow[(cy + j / 3) * kHaloX + cx + j % 3];
+            const float s8 = srow[(cy + 2) * kHaloX + cx + 2];
+            const float sc = inv_sqrt_d * kLog2e;
+            float mx = group_max<8>(j == 0 ? fmaxf(sj, s8) : sj);
+            const float ej = exp2_fast((sj - mx) * sc);
+            const float e8 = exp2_fast((s8 - mx) * sc);
+            const float inv = 1.0f / group_sum<8>(j == 0 ? ej + e8 : ej);
+            sA[cell * kAStride + j] = ej * inv;
+            if (j == 0) sA[cell * kAStride + 8] = e8 * inv;
+        } else {
             float s[9];
 #pragma unroll
             for (int k = 0; k < 9; ++k) s[k] = 0.f;
