@@ -57,12 +57,19 @@ __device__ __forceinline__ float act_of(float v) {
     else return v;
 }
 
+// Marks an accumulator block as (re)defined in accumulator registers here, so the
+// copies to vector registers that the epilogue needs are made next to their uses
+// instead of all 256 right after the last MFMA.
+__device__ __forceinline__ void pin_acc(f32x16& a) { asm volatile("" : "+a"(a)); }
+
 // fp32 epilogue: direct 16-byte stores of 4 consecutive channels per lane.
 template <int kAct>
-__device__ __forceinline__ void store_tile_f32(const f32x16 (&acc)[4][4], float* obase, int ncol) {
+__device__ __forceinline__ void store_tile_f32(f32x16 (&acc)[4][4], float* obase, int ncol) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         float* orow = obase + (long long)j * 32 * ncol;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pin_acc(acc[i][j]);
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -84,7 +91,7 @@ constexpr int kEpiWaveB = 32 * kEpiRowB;
 constexpr int kStoresBf16 = 32;  // global stores per wave per tile (bf16 epilogue)
 
 template <int kAct>
-__device__ __forceinline__ void store_tile_bf16(const f32x16 (&acc)[4][4], bf16_t* obase, int ncol,
+__device__ __forceinline__ void store_tile_bf16(f32x16 (&acc)[4][4], bf16_t* obase, int ncol,
                                                 unsigned char* ep, int lane) {
     const int r32 = lane & 31, half = lane >> 5;
     unsigned char* wp = ep + r32 * kEpiRowB + half * 8;
@@ -95,6 +102,8 @@ __device__ __forceinline__ void store_tile_bf16(const f32x16 (&acc)[4][4], bf16_
     for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
+            pin_acc(acc[2 * p][j]);
+            pin_acc(acc[2 * p + 1][j]);
 #pragma unroll
             for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
@@ -111,23 +120,27 @@ __device__ __forceinline__ void store_tile_bf16(const f32x16 (&acc)[4][4], bf16_
                 const long long uoff = ((long long)(j * 32 + s4 * 8) * ncol + p * 64) * 2;  // uniform
                 *reinterpret_cast<uint4*>(ob + uoff + gl) = v;
             }
+            // One 32-row x 64-column block at a time: converting the whole tile up
+            // front would need 256 more registers.
+            __builtin_amdgcn_sched_barrier(0);
         }
 }
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-// One direct global->LDS load (global_load_lds_dwordx4): 16 bytes per lane from
-// gaddr land at LDS byte address lds_base + 16 * lane. Issued through inline asm:
-// the compiler would otherwise make every later LDS read wait for all such loads
-// still in flight (it cannot tell which stage they fill). The pipeline waits for
-// each slab itself (wait_vm) before the barrier that publishes it.
-__device__ __forceinline__ void dma16(const void* gaddr, unsigned lds_base) {
+// One direct global->LDS load (global_load_lds_dwordx4, SGPR base + 32-bit lane
+// offset): 16 bytes per lane from base + voff land at LDS byte address
+// lds_base + 16 * lane. Issued through inline asm: the compiler would otherwise
+// make every later LDS read wait for all such loads still in flight (it cannot
+// tell which stage they fill). The pipeline waits for each slab itself (wait_vm)
+// before the barrier that publishes it.
+__device__ __forceinline__ void dma16(const void* base, unsigned voff, unsigned lds_base) {
     asm volatile(
         "s_mov_b32 m0, %0\n\t"
         "s_nop 0\n\t"
-        "global_load_lds_dwordx4 %1, off"
+        "global_load_lds_dwordx4 %1, %2"
         :
-        : "s"(lds_base), "v"(gaddr)
+        : "s"(lds_base), "v"(voff), "s"(base)
         : "memory", "m0");
 }
 
@@ -138,20 +151,20 @@ __device__ __forceinline__ unsigned lds_addr(const void* p) {
 // Issues the direct global->LDS loads of slab ks of a tile into the stage at LDS
 // byte address sbase: 32 instructions of 16 rows each; wave w issues row groups
 // w, w+4, ..., w+28 (16 cell groups, then 16 weight groups). x, w: the tile's
-// first cell row and first weight row plus this lane's offset (row lane/4 of the
-// group, the logical chunk that lands in physical chunk lane%4).
+// first cell row and first weight row (uniform); voff: this lane's byte offset
+// (row lane/4 of the group, the logical chunk that lands in physical chunk lane%4).
 __device__ __forceinline__ void issue_slab(const char* x, const char* w, long long row_bytes, int ks,
-                                           int wave, unsigned sbase) {
+                                           int wave, unsigned voff, unsigned sbase) {
     const long long k_off = (long long)ks * kSlabB;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int grp = 4 * j + wave;
-        dma16(x + grp * 16 * row_bytes + k_off, sbase + grp * 1024);
+        dma16(x + grp * 16 * row_bytes + k_off, voff, sbase + grp * 1024);
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int grp = 4 * j + wave;
-        dma16(w + grp * 16 * row_bytes + k_off, sbase + (16 + grp) * 1024);
+        dma16(w + grp * 16 * row_bytes + k_off, voff, sbase + (16 + grp) * 1024);
     }
 }
 
@@ -242,62 +255,91 @@ __device__ __forceinline__ void mfma_group(f32x16 (&acc)[4][4], const Frags& f) 
 struct Walk {
     int tile, next, stride, tile_end, nN, nk;
     long long row_bytes;
-    const char *x_cur, *w_cur;  // this tile's operand rows (+ lane offset)
+    unsigned voff;              // this lane's byte offset within a 16-row load group
+    const char *x_cur, *w_cur;  // this tile's first operand rows
     const char *x_nxt, *w_nxt;  // the next tile's, or this tile's when it is the last
 };
 
-// Operand row pointers of a tile, with the lane's offset folded in.
+// First operand rows of a tile (uniform across the workgroup).
 template <typename T>
-__device__ __forceinline__ void tile_rows(const GemmArgs& g, int tile, int nN, long long lane_off,
-                                          const char** x, const char** w) {
+__device__ __forceinline__ void tile_rows(const GemmArgs& g, int tile, int nN, const char** x,
+                                          const char** w) {
     const int m0 = (tile / nN) * kBM, n0 = (tile % nN) * kBN;
     const long long K = g.K;
-    *x = reinterpret_cast<const char*>(static_cast<const T*>(g.A) + m0 * K) + lane_off;
+    *x = reinterpret_cast<const char*>(static_cast<const T*>(g.A) + m0 * K);
     *w = reinterpret_cast<const char*>(static_cast<const T*>(g.Bt) +
-                                       (long long)(m0 / g.rows_per_batch) * g.bt_batch_stride + n0 * K) +
-         lane_off;
+                                       (long long)(m0 / g.rows_per_batch) * g.bt_batch_stride + n0 * K);
 }
 
 // Scheduling-group masks (LLVM AMDGPU IGroupLP): MFMA and LDS-read instructions.
 constexpr int kSchedMfma = 0x008, kSchedDsRead = 0x100;
 
 // One slab step: slab kt of the current tile sits in stage S and its fragments in
-// `cur`. Waits for slab kt+1, issues the 8 direct loads of slab kt+4 into stage S
-// and the 16 fragment reads of slab kt+1 (stage (S+1)%4, into `nxt`) interleaved
-// with the first 8 of the 32 MFMA groups of slab kt, then the other 24: the
-// reads land while the matrix cores work, and nothing waits for LDS inside the
-// step. Past the last slab of the last tile the reads pick up stale stage data
-// and the loads refetch a valid slab, so every step issues the same instructions
-// and the vmcnt bookkeeping stays uniform.
-template <typename T, int S, bool kFirstSlab>
+// `f` (one register set per 32-byte half kk). The MFMAs of half 0 go first; then
+// the step waits for slab kt+1 and meets the other waves (after which stage S is
+// free), issues the 8 direct loads of slab kt+4 into stage S, and reads slab
+// kt+1's half-0 fragments into the half-0 registers while the half-1 MFMAs run,
+// then its half-1 fragments (consumed in the next step's second half). The
+// matrix cores keep working through the barrier and nothing waits for LDS inside
+// the step. The last step of a tile reads nothing: slab 0 of the next tile is
+// read after the epilogue. Past the last slab of the last tile the loads refetch
+// a valid slab, so every step issues the same loads and the vmcnt bookkeeping
+// stays uniform.
+template <typename T, int S, bool kFirstSlab, bool kReadNext>
 __device__ __forceinline__ void slab_step(const Walk& wk, int kt, int wave, unsigned char* lds,
-                                          const FragBase& fb, f32x16 (&acc)[4][4], const Frags& cur,
-                                          Frags& nxt, int younger) {
+                                          const FragBase& fb, f32x16 (&acc)[4][4], Frags& f,
+                                          int younger) {
+    constexpr int kPer = sizeof(T) == 2 ? 1 : 4;  // MFMA instructions per group
     __builtin_amdgcn_sched_barrier(0);
+    static_for<0, 16>([&](auto m) {
+        constexpr int M = decltype(m)::value;
+        mfma_group<T, kFirstSlab, M>(acc, f);
+    });
     wait_vm(younger);
     lds_barrier();  // slab kt+1 is in LDS; every wave is done reading stage S
     const int ks = kt + 4;
     const bool same = ks < wk.nk;
     issue_slab(same ? wk.x_cur : wk.x_nxt, same ? wk.w_cur : wk.w_nxt, wk.row_bytes,
-               same ? ks : ks - wk.nk, wave, lds_addr(lds + S * kStageB));
+               same ? ks : ks - wk.nk, wave, wk.voff, lds_addr(lds + S * kStageB));
     const unsigned char* rd = lds + ((S + 1) & 3) * kStageB;
-    static_for<0, 16>([&](auto r) { read_frag<decltype(r)::value>(nxt, rd, fb); });
-    static_for<0, 32>([&](auto m) {
+    if constexpr (kReadNext)
+        static_for<0, 8>([&](auto r) { read_frag<decltype(r)::value>(f, rd, fb); });
+    static_for<16, 32>([&](auto m) {
         constexpr int M = decltype(m)::value;
-        mfma_group<T, kFirstSlab && M < 16, M>(acc, cur);
+        mfma_group<T, false, M>(acc, f);
     });
-    static_for<0, 8>([&](auto) {
-        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
-        __builtin_amdgcn_sched_group_barrier(kSchedMfma, sizeof(T) == 2 ? 1 : 4, 0);
-    });
-    __builtin_amdgcn_sched_group_barrier(kSchedMfma, sizeof(T) == 2 ? 24 : 96, 0);
+    if constexpr (kReadNext) {
+        static_for<8, 16>([&](auto r) { read_frag<decltype(r)::value>(f, rd, fb); });
+        static_for<0, 8>([&](auto) {
+            __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2 * kPer, 0);
+        });
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 8, 0);
+    }
     __builtin_amdgcn_sched_barrier(0);
+}
+
+// Four slab steps kb..kb+3 (stages 0..3). kFirst: the tile's first group (zero
+// start, and after an epilogue the stores count as younger than slabs 1..3);
+// kLast: the tile's last group (its last step reads no next fragments).
+template <typename T, bool kFirst, bool kLast>
+__device__ __forceinline__ void slab_group(const Walk& wk, int kb, int wave, unsigned char* lds,
+                                           const FragBase& fb, f32x16 (&acc)[4][4], Frags& f,
+                                           int y_first) {
+    constexpr int y = 2 * kDmaPerSlab;
+    slab_step<T, 0, kFirst, true>(wk, kb + 0, wave, lds, fb, acc, f, kFirst ? y_first : y);
+    slab_step<T, 1, false, true>(wk, kb + 1, wave, lds, fb, acc, f, kFirst ? y_first : y);
+    slab_step<T, 2, false, true>(wk, kb + 2, wave, lds, fb, acc, f, kFirst ? y_first : y);
+    slab_step<T, 3, false, !kLast>(wk, kb + 3, wave, lds, fb, acc, f, y);
 }
 
 template <typename T>
 __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs g) {
     __shared__ __attribute__((aligned(1024))) unsigned char lds[4 * kStageB];
     constexpr bool kBf16 = sizeof(T) == 2;
+    // bf16 epilogue staging, one region per wave (the stages hold the next tile's
+    // first slabs while the epilogue runs).
+    __shared__ __attribute__((aligned(16))) unsigned char epi[kBf16 ? 4 * kEpiWaveB : 16];
     constexpr int kStores = kBf16 ? kStoresBf16 : kStoresF32;
     constexpr int kSlabE = kSlabB / (int)sizeof(T);
 
@@ -315,7 +357,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs g) {
     // first row is a multiple of 32 for even waves and 16 more for odd ones.
     const int dma_row = lane >> 2;
     const int dma_chunk = (lane & 3) ^ row_swz(16 * (wave & 1) + dma_row);
-    const long long lane_off = dma_row * wk.row_bytes + dma_chunk * 16;
+    wk.voff = (unsigned)(dma_row * wk.row_bytes + dma_chunk * 16);
     const int ntiles = (g.M / kBM) * wk.nN;
     if ((gridDim.x & 7) == 0) {
         const int per_xcd_wg = gridDim.x >> 3;
@@ -341,61 +383,80 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs g) {
     }
 
     // Prologue: slabs 0..3 of the first tile, then slab 0's fragments.
-    tile_rows<T>(g, wk.tile, wk.nN, lane_off, &wk.x_cur, &wk.w_cur);
+    tile_rows<T>(g, wk.tile, wk.nN, &wk.x_cur, &wk.w_cur);
 #pragma unroll
-    for (int s = 0; s < 4; ++s) issue_slab(wk.x_cur, wk.w_cur, wk.row_bytes, s, wave, lds_addr(lds + s * kStageB));
+    for (int s = 0; s < 4; ++s)
+        issue_slab(wk.x_cur, wk.w_cur, wk.row_bytes, s, wave, wk.voff, lds_addr(lds + s * kStageB));
     wait_vm(3 * kDmaPerSlab);
     lds_barrier();
-    Frags fa, fb;
+    Frags fa;
     static_for<0, 16>([&](auto r) { read_frag<decltype(r)::value>(fa, lds, fbase); });
 
     bool stores_pending = false;  // the previous tile's stores follow slabs 0..3 of this one
     f32x16 acc[4][4];
     while (true) {
         wk.next = wk.tile + wk.stride < wk.tile_end ? wk.tile + wk.stride : -1;
-        if (wk.next >= 0) tile_rows<T>(g, wk.next, wk.nN, lane_off, &wk.x_nxt, &wk.w_nxt);
+        if (wk.next >= 0) tile_rows<T>(g, wk.next, wk.nN, &wk.x_nxt, &wk.w_nxt);
         else wk.x_nxt = wk.x_cur, wk.w_nxt = wk.w_cur;
         // Loads younger than slab kt+1 when step kt waits for it: slabs kt+2 and
         // kt+3, and for kt <= 2 after an epilogue also that epilogue's stores.
         constexpr int y_store = kStores + 2 * kDmaPerSlab <= 63 ? kStores + 2 * kDmaPerSlab : 0;
         const int y_first = stores_pending ? y_store : 2 * kDmaPerSlab;
-        slab_step<T, 0, true>(wk, 0, wave, lds, fbase, acc, fa, fb, y_first);
-        slab_step<T, 1, false>(wk, 1, wave, lds, fbase, acc, fb, fa, y_first);
-        slab_step<T, 2, false>(wk, 2, wave, lds, fbase, acc, fa, fb, y_first);
-        slab_step<T, 3, false>(wk, 3, wave, lds, fbase, acc, fb, fa, 2 * kDmaPerSlab);
-        for (int kb = 4; kb < wk.nk; kb += 4) {
-            slab_step<T, 0, false>(wk, kb + 0, wave, lds, fbase, acc, fa, fb, 2 * kDmaPerSlab);
-            slab_step<T, 1, false>(wk, kb + 1, wave, lds, fbase, acc, fb, fa, 2 * kDmaPerSlab);
-            slab_step<T, 2, false>(wk, kb + 2, wave, lds, fbase, acc, fa, fb, 2 * kDmaPerSlab);
-            slab_step<T, 3, false>(wk, kb + 3, wave, lds, fbase, acc, fb, fa, 2 * kDmaPerSlab);
+        if (wk.nk == 4) {
+            slab_group<T, true, true>(wk, 0, wave, lds, fbase, acc, fa, y_first);
+        } else {
+            slab_group<T, true, false>(wk, 0, wave, lds, fbase, acc, fa, y_first);
+            for (int kb = 4; kb < wk.nk - 4; kb += 4)
+                slab_group<T, false, false>(wk, kb, wave, lds, fbase, acc, fa, 0);
+            slab_group<T, false, true>(wk, wk.nk - 4, wave, lds, fbase, acc, fa, 0);
         }
-        // fa now holds slab 0 of the next tile (stage 0). Stage 0 becomes the
-        // epilogue's staging area once every wave has read it.
+        // Slab 0 of the next tile is in stage 0 (published by the last step's barrier);
+        // its fragments are read after the epilogue.
         const int m0 = (wk.tile / wk.nN) * kBM, n0 = (wk.tile % wk.nN) * kBN;
         const int plane = n0 / g.ncol;
         T* out = static_cast<T*>(g.out[plane]);
         const int col0 = n0 - plane * g.ncol + wn * 128;
         // The whole 256-wide N tile lies in one output plane: uniform activation.
         if constexpr (kBf16) {
-            lds_barrier();
-            unsigned char* ep = lds + wave * kEpiWaveB;
+            unsigned char* ep = epi + wave * kEpiWaveB;
             bf16_t* obase = reinterpret_cast<bf16_t*>(out) + (long long)(m0 + wm * 128) * g.ncol + col0;
+            // The distinct markers keep the compiler from hoisting the accumulator
+            // reads common to the three arms above the switch (all 256 at once).
             switch (g.act[plane]) {
-                case 1: store_tile_bf16<1>(acc, obase, g.ncol, ep, lane); break;
-                case 2: store_tile_bf16<2>(acc, obase, g.ncol, ep, lane); break;
-                default: store_tile_bf16<0>(acc, obase, g.ncol, ep, lane); break;
+                case 1:
+                    asm volatile("; epilogue relu");
+                    store_tile_bf16<1>(acc, obase, g.ncol, ep, lane);
+                    break;
+                case 2:
+                    asm volatile("; epilogue gelu");
+                    store_tile_bf16<2>(acc, obase, g.ncol, ep, lane);
+                    break;
+                default:
+                    asm volatile("; epilogue identity");
+                    store_tile_bf16<0>(acc, obase, g.ncol, ep, lane);
+                    break;
             }
         } else {
             float* obase = reinterpret_cast<float*>(out) + (long long)(m0 + wm * 128 + r32) * g.ncol +
                            col0 + 4 * half;
             switch (g.act[plane]) {
-                case 1: store_tile_f32<1>(acc, obase, g.ncol); break;
-                case 2: store_tile_f32<2>(acc, obase, g.ncol); break;
-                default: store_tile_f32<0>(acc, obase, g.ncol); break;
+                case 1:
+                    asm volatile("; epilogue relu");
+                    store_tile_f32<1>(acc, obase, g.ncol);
+                    break;
+                case 2:
+                    asm volatile("; epilogue gelu");
+                    store_tile_f32<2>(acc, obase, g.ncol);
+                    break;
+                default:
+                    asm volatile("; epilogue identity");
+                    store_tile_f32<0>(acc, obase, g.ncol);
+                    break;
             }
         }
         stores_pending = true;
         if (wk.next < 0) break;
+        static_for<0, 16>([&](auto r) { read_frag<decltype(r)::value>(fa, lds, fbase); });
         wk.tile = wk.next;
         wk.x_cur = wk.x_nxt;
         wk.w_cur = wk.w_nxt;
