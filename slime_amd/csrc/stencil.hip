@@ -161,11 +161,6 @@ __device__ __forceinline__ float group_max(float v) {
     return v;
 }
 
-// Score matrix of the MFMA score phase: 32 tile cells x 64 halo rows, fp32, rows
-// padded to 72 floats so the two half-waves of an MFMA result write (rows m and
-// m+4) land in different banks.
-constexpr int kScoreLd = 72;
-
 // TY: storage type of the unscaled output; fp32 when the caller rescales it into
 // the final bf16 state (one rounding instead of two).
 template <typename T, int D, typename TY>
@@ -179,11 +174,6 @@ __global__ __launch_bounds__((Layout<T, D>::kThreads), 2) void stencil_kernel(St
     __shared__ __attribute__((aligned(16))) unsigned char bufA[L::kBufB];
     __shared__ __attribute__((aligned(16))) unsigned char bufB[L::kBufB];
     __shared__ __attribute__((aligned(16))) float sAtt[2][kTileCells * kAStride];
-    // bf16, D = 64 (256 threads, 8 per cell): the scores <P, I> of all 32 cells
-    // against all 64 staged halo rows come from the matrix cores (v_mfma
-    // 32x32x16), 9 of each row are used.
-    constexpr bool kMfmaScores = sizeof(T) == 2 && D == 64;
-    __shared__ __attribute__((aligned(16))) float sS[kMfmaScores ? kTileCells * kScoreLd : 1];
     __shared__ __attribute__((aligned(16))) float sMS[H * kTileCells * 2];
     __shared__ float sR[L::kWaves * 16];
 
@@ -319,45 +309,7 @@ __global__ __launch_bounds__((Layout<T, D>::kThreads), 2) void stencil_kernel(St
         if (h + 1 < H) issue_head(h + 1, nxt);
 
         // ---- phase A: attention scores (S4) and softmax --------------------------------
-        if constexpr (kMfmaScores) {
-            // Waves 0 and 1: S[cell][n] = <P_cell, I_n> for halo rows n of block 32*wave,
-            // K = D channels in steps of 16. A = P (row = cell), B = I^T (column = halo
-            // row); both operands are 16-byte chunks of swizzled rows.
-            if (wave < 2) {
-                const int m = lane & 31, kh = lane >> 5;
-                const int n = 32 * wave + m;
-                f32x16 acc = {};
-#pragma unroll
-                for (int ks = 0; ks < D / 16; ++ks) {
-                    const int c = 2 * ks + kh;
-                    const uint4 pa = *reinterpret_cast<const uint4*>(
-                        buf + L::offP + m * L::kRowB + ((c ^ (m & L::kSwz)) << 4));
-                    const uint4 ib = *reinterpret_cast<const uint4*>(
-                        buf + L::offI + n * L::kRowB + ((c ^ (n & L::kSwz)) << 4));
-                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_v, pa),
-                                                                  __builtin_bit_cast(bf16x8_v, ib), acc,
-                                                                  0, 0, 0);
-                }
-#pragma unroll
-                for (int e = 0; e < 16; ++e)
-                    sS[(8 * (e >> 2) + 4 * kh + (e & 3)) * kScoreLd + n] = acc[e];
-            }
-            lds_barrier();
-            // Softmax over the 9 neighbours: 8 lanes per cell, lane j takes neighbour j,
-            // lane 0 also neighbour 8.
-            const int cell = tid >> 3, j = tid & 7;
-            const int cy = cell / kTileX, cx = cell % kTileX;
-            const float* srow = sS + cell * kScoreLd;
-            const float sj = srow[(cy + j / 3) * kHaloX + cx + j % 3];
-            const float s8 = srow[(cy + 2) * kHaloX + cx + 2];
-            const float sc = inv_sqrt_d * kLog2e;
-            float mx = group_max<8>(j == 0 ? fmaxf(sj, s8) : sj);
-            const float ej = exp2_fast((sj - mx) * sc);
-            const float e8 = exp2_fast((s8 - mx) * sc);
-            const float inv = 1.0f / group_sum<8>(j == 0 ? ej + e8 : ej);
-            sA[cell * kAStride + j] = ej * inv;
-            if (j == 0) sA[cell * kAStride + 8] = e8 * inv;
-        } else {
+        {
             float s[9];
 #pragma unroll
             for (int k = 0; k < 9; ++k) s[k] = 0.f;
@@ -521,6 +473,467 @@ __global__ __launch_bounds__((Layout<T, D>::kThreads), 2) void stencil_kernel(St
     }
 }
 
+// ---- bf16 state, D = 64: the neighbourhood sums on the matrix cores ------------------
+//
+// Same tiles and outputs as stencil_kernel, but S2 and S5 -- the two 9-tap sums per
+// (cell, channel) that dominate the generic kernel's VALU work -- become MFMA
+// products over the staged halo:
+//   U^T  = X_halo^T . Kmat^T      Kmat[cell][n] = K[h][k] if halo row n = n_k(cell)
+//   Vt^T = V_halo^T . Att^T       Att[cell][n]  = a_k(cell) likewise (0 elsewhere)
+// (M = 16 channels, N = 16 cells, K = 64 halo rows; v_mfma_f32_16x16x32_bf16).
+// The sparse 32 x 64 weight matrices live in LDS; each head rewrites only their 9
+// non-zeros per cell. Weights enter as bf16 hi + lo pairs (w = hi + lo to 2^-17
+// relative) and X, V are bf16 already, so every product is exact in fp32 and the
+// sums keep fp32 accuracy. The halo^T operands come straight from the row-major
+// halo through ds_read_b64_tr_b16 (gfx950's transposing LDS read).
+//
+// Per head: each wave computes 16 cells x 32 halo rows of the scores <P, I> on the
+// matrix cores and keeps the 9 per cell that are neighbours; all lanes run the
+// softmax (8 per cell) and write the weights; each wave then owns 16 channels of
+// all 32 cells for growth, update and head mixing in registers.
+//
+// The kernel is persistent: a workgroup walks a run of tiles (XCD-contiguous), and
+// the staging pipeline runs across tile boundaries -- head 0 of the next tile and
+// that tile's parameters are in flight while the last head of the current one
+// computes -- so no workgroup starts from an empty pipeline.
+namespace mf {
+
+constexpr int kD = 64;
+constexpr int kRowB = kD * 2;                          // bytes per (cell, head) row
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int offX = 0, offV = kHaloPad * kRowB, offI = 2 * kHaloPad * kRowB,
+              offP = 3 * kHaloPad * kRowB;
+constexpr int kBufB = (3 * kHaloPad + kTileCells) * kRowB;  // 28 KiB
+constexpr int kMatB = kTileCells * kRowB;                    // one 32 x 64 bf16 weight matrix
+constexpr int kS9 = 12;                                      // floats per cell in the score buffer
+// Per-tile parameter block (fp32): K[8][9], M[8][8] (M[o][h] at o*8+h), mu[8],
+// sigma[8], scale[8]; then, for per-cell growth, mu and sigma [cell][8].
+constexpr int kPK = 0, kPM = 72, kPMu = 136, kPSg = 144, kPSc = 152, kPScal = 160;
+constexpr int kPCellMu = 160, kPCellSg = 160 + kTileCells * 8, kParF = 160 + 2 * kTileCells * 8;
+
+// 16-byte chunk swizzles inside a 128-byte row. X and V: any four consecutive
+// rows 4j..4j+3, and rows {r, r+2, r+8, r+10}, occupy disjoint chunk pairs, so
+// the transposing reads (4 rows x 32 bytes per 16 lanes) are free of bank
+// conflicts. I and P: chunk ^ (row & 7).
+__device__ __forceinline__ int swz_xv(int row) { return 2 * ((row ^ (row >> 3)) & 3); }
+__device__ __forceinline__ int swz_ip(int row) { return row & 7; }
+
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane i receives element i % 4 of
+// the 8 bytes read by lanes i/4, 4 + i/4, 8 + i/4, 12 + i/4 (in that order).
+__device__ __forceinline__ uint2 read_tr16(const unsigned char* p) {
+    const v4i16 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_v4i16*)(const __attribute__((address_space(3))) unsigned char*)(p));
+    return __builtin_bit_cast(uint2, v);
+}
+
+__device__ __forceinline__ f32x4 mfma16(uint4 a, uint4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_v, a),
+                                                  __builtin_bit_cast(bf16x8_v, b), c, 0, 0, 0);
+}
+
+// hi + lo bf16 split of an fp32 weight.
+__device__ __forceinline__ void split_bf16(float v, bf16_t& hi, bf16_t& lo) {
+    hi = f32_to_bf16(v);
+    lo = f32_to_bf16(v - bf16_to_f32(hi));
+}
+
+// One step of a butterfly sum of kN*2 per-lane values: lanes whose bit `bit` is
+// set keep the upper half, the others the lower half, each adding the partner
+// lane's copy (DPP kCtrl, whose partner differs from the lane in that bit and in
+// no bit a previous step used).
+template <int kN, int kCtrl>
+__device__ __forceinline__ void fold_half(float (&v)[16], int lane, int bit) {
+    const bool up = (lane >> bit) & 1;
+#pragma unroll
+    for (int i = 0; i < kN; ++i) {
+        const float keep = up ? v[i + kN] : v[i];
+        const float send = up ? v[i] : v[i + kN];
+        v[i] = keep + dpp_f32<kCtrl>(send);
+    }
+}
+
+}  // namespace mf
+
+template <typename TY>
+__global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilArgs a) {
+    using namespace mf;
+    constexpr int H = kHeads;
+    constexpr int C = H * kD;
+    __shared__ __attribute__((aligned(16))) unsigned char bufA[kBufB];
+    __shared__ __attribute__((aligned(16))) unsigned char bufB[kBufB];
+    // Weight matrices [cell][halo row] bf16, chunk-swizzled by cell & 7:
+    // 0 = K hi, 1 = K lo, 2 = a hi, 3 = a lo.
+    __shared__ __attribute__((aligned(16))) unsigned char sW[4 * kMatB];
+    __shared__ __attribute__((aligned(16))) float sS9[kTileCells * kS9 + kThreads];  // + discard slots
+    // One parameter block: a tile's block is written after the barrier that ends
+    // the previous tile's last head, its last reader.
+    __shared__ __attribute__((aligned(16))) float sPar[kParF];
+    __shared__ float sR[kThreads];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int G = a.G;
+    const int tiles_x = G / kTileX;
+    const int tpb = (G / kTileY) * tiles_x;
+    const int ntiles = a.B * tpb;
+
+    // ---- this workgroup's tiles: an XCD-contiguous run --------------------------------
+    int t_cur, t_stride, t_end;
+    if ((gridDim.x & 7) == 0 && (ntiles & 7) == 0) {
+        const int span = ntiles >> 3;
+        t_cur = (blockIdx.x & 7) * span + (blockIdx.x >> 3);
+        t_stride = gridDim.x >> 3;
+        t_end = (blockIdx.x & 7) * span + span;
+    } else {
+        t_cur = blockIdx.x;
+        t_stride = gridDim.x;
+        t_end = ntiles;
+    }
+    if (t_cur >= t_end) return;
+
+    // ---- staging: 8 halo rows (or P rows) per direct-load instruction -------------------
+    // Lane l of an instruction lands at row g*8 + l/8, physical chunk l%8, and fetches
+    // the logical chunk the row's swizzle maps there. Wave w issues groups w and w+4
+    // of each halo array and group w of the P tile.
+    unsigned boff_xv[2], boff_i[2], boff_p;
+    const char *srcX, *srcV, *srcI, *srcP;
+    auto set_tile = [&](int t) {  // per-lane offsets and bases of tile t
+        const int b = t / tpb, tile = t % tpb;
+        const int ty0 = (tile / tiles_x) * kTileY, tx0 = (tile % tiles_x) * kTileX;
+        const int pc = lane & 7;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int row = (wave + 4 * k) * 8 + (lane >> 3);
+            const int gc = row < kHaloCells ? row : kHaloCells - 1;  // padding rows
+            const int gy = wrapi(ty0 + gc / kHaloX - 1, G), gx = wrapi(tx0 + gc % kHaloX - 1, G);
+            const int base = (gy * G + gx) * C;
+            boff_xv[k] = (unsigned)(base + (pc ^ swz_xv(row)) * 8) * 2u;
+            boff_i[k] = (unsigned)(base + (pc ^ swz_ip(row)) * 8) * 2u;
+        }
+        const int row = wave * 8 + (lane >> 3);  // tile cell
+        const int base = ((ty0 + row / kTileX) * G + tx0 + row % kTileX) * C;
+        boff_p = (unsigned)(base + (pc ^ swz_ip(row)) * 8) * 2u;
+        const long long bb = (long long)b * G * G * C;
+        srcX = reinterpret_cast<const char*>(static_cast<const bf16_t*>(a.X) + bb);
+        srcV = reinterpret_cast<const char*>(static_cast<const bf16_t*>(a.V) + bb);
+        srcI = reinterpret_cast<const char*>(static_cast<const bf16_t*>(a.I) + bb);
+        srcP = reinterpret_cast<const char*>(static_cast<const bf16_t*>(a.P) + bb);
+    };
+    auto issue_head = [&](int h, unsigned char* buf) {
+        const unsigned hb = (unsigned)(h * kRowB);
+        const unsigned lb = lds_addr(buf);
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const unsigned row = lb + (wave + 4 * k) * 1024;
+            dma16_saddr(srcX, boff_xv[k] + hb, row + offX);
+            dma16_saddr(srcV, boff_xv[k] + hb, row + offV);
+            dma16_saddr(srcI, boff_i[k] + hb, row + offI);
+        }
+        dma16_saddr(srcP, boff_p + hb, lb + offP + wave * 1024);
+    };
+    // Per-tile parameters: up to three floats per lane, loaded into registers with
+    // the tile's first staging and written to LDS once they have landed.
+    float pre[3];
+    auto fetch_params = [&](int t) {
+        const int b = t / tpb, tile = t % tpb;
+        const int pod = b / a.per_pod;
+        pre[0] = pre[1] = pre[2] = 0.f;
+        if (tid < kPK + 72) pre[0] = a.K[pod * 72 + tid];
+        else if (tid < kPM + 64) pre[0] = a.M[pod * 64 + tid - kPM];
+        else if (tid < kPSg + 8) {
+            if (!a.per_cell) pre[0] = tid < kPSg ? a.mu[pod * 8 + tid - kPMu] : a.sigma[pod * 8 + tid - kPSg];
+        } else if (tid < kPScal) {
+            pre[0] = a.scale_in ? a.scale_in[b * 8 + tid - kPSc] : 1.0f;
+        }
+        if (a.per_cell) {
+            const int ty0 = (tile / tiles_x) * kTileY, tx0 = (tile % tiles_x) * kTileX;
+            const int cell = tid >> 3, hh = tid & 7;
+            const long long pi =
+                (((long long)pod * G + ty0 + cell / kTileX) * G + tx0 + cell % kTileX) * H + hh;
+            pre[1] = a.mu[pi];
+            pre[2] = a.sigma[pi];
+        }
+    };
+    auto store_params = [&](float* par) {
+        if (tid < kPScal) par[tid] = pre[0];
+        if (a.per_cell) {
+            par[kPCellMu + tid] = pre[1];
+            par[kPCellSg + tid] = pre[2];
+        }
+    };
+
+    // The weight matrices are zero except at the 9 neighbours of each cell.
+    for (int i = tid; i < 4 * kMatB / 16; i += kThreads)
+        reinterpret_cast<uint4*>(sW)[i] = make_uint4(0u, 0u, 0u, 0u);
+    set_tile(t_cur);
+    fetch_params(t_cur);
+    issue_head(0, bufA);
+
+    // ---- per-lane roles (tile independent) ----------------------------------------------
+    const int grp = lane >> 4, i16 = lane & 15;
+    // softmax: cell sc, neighbour sj (lane sj == 0 also takes neighbour 8)
+    const int sc = tid >> 3, sj = tid & 7;
+    auto wpos = [&](int k) {  // byte offset of (cell sc, neighbour k) in a weight matrix
+        const int scy = sc / kTileX, scx = sc % kTileX;
+        const int n = (scy + k / 3) * kHaloX + scx + k % 3;
+        return sc * kRowB + (((n >> 3) ^ (sc & 7)) << 4) + (n & 7) * 2;
+    };
+    const int wp_j = wpos(sj), wp_8 = wpos(8);
+    // scores: this wave's 16 cells (block cb) x 32 halo rows (block hb), as two
+    // 16 x 16 blocks j; A = P rows, B = I rows, K = channels.
+    const int cb = wave >> 1, hb = wave & 1;
+    unsigned sp_off[2], si_off[2][2], s9_off[2][4];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+        const int cell = 16 * cb + i16;
+        sp_off[ks] = (unsigned)(offP + cell * kRowB + (((4 * ks + grp) ^ swz_ip(cell)) << 4));
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int n = 32 * hb + 16 * j + i16;
+            si_off[j][ks] = (unsigned)(offI + n * kRowB + (((4 * ks + grp) ^ swz_ip(n)) << 4));
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            // result (j, e): cell 16 cb + 4 grp + e, halo row n = 32 hb + 16 j + i16
+            const int cell = 16 * cb + 4 * grp + e, n = 32 * hb + 16 * j + i16;
+            const int dy = n / kHaloX - cell / kTileX, dx = n % kHaloX - cell % kTileX;
+            const bool keep = n < kHaloCells && (unsigned)dy < 3u && (unsigned)dx < 3u;
+            s9_off[j][e] = (unsigned)(keep ? cell * kS9 + 3 * dy + dx : kTileCells * kS9 + tid) * 4u;
+        }
+    // phase B: channels 16 wave + 4 grp .. +3 of cells 16 nb + i16.
+    const int ch0 = 16 * wave + 4 * grp;
+    unsigned tr_off[2][2];  // halo row 32 ks + 8 grp + 4 hf + i16/4, channels 16 wave + 4 (i16 % 4)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+            const int row = 32 * ks + 8 * grp + 4 * hf + (i16 >> 2);
+            const int q = i16 & 3;
+            tr_off[ks][hf] = (unsigned)(row * kRowB + (((2 * wave + (q >> 1)) ^ swz_xv(row)) << 4) +
+                                        8 * (q & 1));
+        }
+    unsigned w_off[2][2];  // cell 16 nb + i16, halo rows 32 ks + 8 grp .. +7
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const int cell = 16 * nb + i16;
+            w_off[nb][ks] = (unsigned)(cell * kRowB + (((4 * ks + grp) ^ (cell & 7)) << 4));
+        }
+    unsigned xc_off[2];  // centre row of cell 16 nb + i16, channels ch0 .. ch0+3
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+        const int cell = 16 * nb + i16;
+        const int crow = (cell / kTileX + 1) * kHaloX + cell % kTileX + 1;
+        xc_off[nb] = (unsigned)(offX + crow * kRowB + (((2 * wave + (grp >> 1)) ^ swz_xv(crow)) << 4) +
+                                8 * (grp & 1));
+    }
+
+    constexpr float kLog2e = 1.4426950408889634f;
+    const float score_scale = kLog2e / 8.0f;  // log2(e) / sqrt(D)
+    const float sqrt_log2e = __builtin_sqrtf(kLog2e);
+    const float dt = a.dt;
+
+    float y[H][2][4];
+    float xin[H];
+    int gh = 0;  // heads processed by this workgroup (selects the staging buffer)
+    while (true) {
+        const int t_next = t_cur + t_stride < t_end ? t_cur + t_stride : -1;
+        const int b = t_cur / tpb, tile = t_cur % tpb;
+        const int ty0 = (tile / tiles_x) * kTileY, tx0 = (tile % tiles_x) * kTileX;
+        const long long bbase = (long long)b * G * G * C;
+        float* par = sPar;
+#pragma unroll
+        for (int o = 0; o < H; ++o) {
+            xin[o] = 0.f;
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) y[o][nb][e] = 0.f;
+        }
+
+        for (int h = 0; h < H; ++h, ++gh) {
+            const unsigned char* buf = (gh & 1) ? bufB : bufA;
+            unsigned char* nxt = (gh & 1) ? bufA : bufB;
+            wait_vm0();       // this wave's loads of head h have landed
+            __syncthreads();  // ... and every other wave's; head h-1 is fully consumed
+            if (h == 0) store_params(par);
+            if (h + 1 < H) {
+                issue_head(h + 1, nxt);
+            } else if (t_next >= 0) {
+                set_tile(t_next);
+                fetch_params(t_next);
+                issue_head(0, nxt);
+            }
+
+            // ---- S4 scores: S[cell][n] = <P_cell, I_n>, kept for the 9 neighbours --------
+            {
+                const uint4 pa0 = *reinterpret_cast<const uint4*>(buf + sp_off[0]);
+                const uint4 pa1 = *reinterpret_cast<const uint4*>(buf + sp_off[1]);
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+                    acc = mfma16(pa0, *reinterpret_cast<const uint4*>(buf + si_off[j][0]), acc);
+                    acc = mfma16(pa1, *reinterpret_cast<const uint4*>(buf + si_off[j][1]), acc);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        *reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(sS9) + s9_off[j][e]) =
+                            acc[e];
+                }
+            }
+            lds_barrier();
+
+            // ---- softmax and the weight matrices of this head -----------------------------
+            {
+                const float* srow = sS9 + sc * kS9;
+                const float s_j = srow[sj], s_8 = srow[8];
+                const float mx = group_max<8>(sj == 0 ? fmaxf(s_j, s_8) : s_j);
+                const float e_j = exp2_fast((s_j - mx) * score_scale);
+                const float e_8 = exp2_fast((s_8 - mx) * score_scale);
+                const float inv = rcp_fast(group_sum<8>(sj == 0 ? e_j + e_8 : e_j));
+                bf16_t hi, lo;
+                split_bf16(par[kPK + h * 9 + sj], hi, lo);
+                *reinterpret_cast<bf16_t*>(sW + 0 * kMatB + wp_j) = hi;
+                *reinterpret_cast<bf16_t*>(sW + 1 * kMatB + wp_j) = lo;
+                split_bf16(e_j * inv, hi, lo);
+                *reinterpret_cast<bf16_t*>(sW + 2 * kMatB + wp_j) = hi;
+                *reinterpret_cast<bf16_t*>(sW + 3 * kMatB + wp_j) = lo;
+                if (sj == 0) {
+                    split_bf16(par[kPK + h * 9 + 8], hi, lo);
+                    *reinterpret_cast<bf16_t*>(sW + 0 * kMatB + wp_8) = hi;
+                    *reinterpret_cast<bf16_t*>(sW + 1 * kMatB + wp_8) = lo;
+                    split_bf16(e_8 * inv, hi, lo);
+                    *reinterpret_cast<bf16_t*>(sW + 2 * kMatB + wp_8) = hi;
+                    *reinterpret_cast<bf16_t*>(sW + 3 * kMatB + wp_8) = lo;
+                }
+            }
+            lds_barrier();
+
+            // ---- S2 / S5 on the matrix cores, then S3, S6 and head mixing -----------------
+            {
+                uint4 ax[2], av[2];
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks) {
+                    const uint2 x0 = read_tr16(buf + offX + tr_off[ks][0]);
+                    const uint2 x1 = read_tr16(buf + offX + tr_off[ks][1]);
+                    const uint2 v0 = read_tr16(buf + offV + tr_off[ks][0]);
+                    const uint2 v1 = read_tr16(buf + offV + tr_off[ks][1]);
+                    ax[ks] = make_uint4(x0.x, x0.y, x1.x, x1.y);
+                    av[ks] = make_uint4(v0.x, v0.y, v1.x, v1.y);
+                }
+                f32x4 u[2], vt[2];
+#pragma unroll
+                for (int nb = 0; nb < 2; ++nb) u[nb] = vt[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                    for (int m = 0; m < 2; ++m)  // hi, lo
+#pragma unroll
+                        for (int nb = 0; nb < 2; ++nb) {
+                            u[nb] = mfma16(ax[ks], *reinterpret_cast<const uint4*>(sW + m * kMatB + w_off[nb][ks]),
+                                           u[nb]);
+                            vt[nb] = mfma16(av[ks],
+                                            *reinterpret_cast<const uint4*>(sW + (2 + m) * kMatB + w_off[nb][ks]),
+                                            vt[nb]);
+                        }
+                const float s_in = par[kPSc + h];  // deferred mass scale of X
+                const float two_dt = 2.0f * dt;
+                float mw[H];
+#pragma unroll
+                for (int o = 0; o < H; ++o) mw[o] = par[kPM + o * H + h];
+                float ga[2], gb[2];  // (U s - mu) / (sigma + 1e-7) * sqrt(log2 e) = U ga - gb
+                if (a.per_cell) {
+#pragma unroll
+                    for (int nb = 0; nb < 2; ++nb) {
+                        const int cell = 16 * nb + i16;
+                        const float g = sqrt_log2e / (par[kPCellSg + cell * 8 + h] + 1e-7f);
+                        ga[nb] = g * s_in;
+                        gb[nb] = par[kPCellMu + cell * 8 + h] * g;
+                    }
+                } else {
+                    const float g = sqrt_log2e / (par[kPSg + h] + 1e-7f);
+                    ga[0] = ga[1] = g * s_in;
+                    gb[0] = gb[1] = par[kPMu + h] * g;
+                }
+                float xacc = 0.f;
+#pragma unroll
+                for (int nb = 0; nb < 2; ++nb) {
+                    const uint2 xr = *reinterpret_cast<const uint2*>(buf + xc_off[nb]);
+                    const float xv[4] = {bf16lo(xr.x), bf16hi(xr.x), bf16lo(xr.y), bf16hi(xr.y)};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float tg = __builtin_fmaf(u[nb][e], ga[nb], -gb[nb]);
+                        const float ex = exp2_fast(-tg * tg);
+                        const float coef = __builtin_fmaf(ex, two_dt, -dt);  // dt * g
+                        const float xc = xv[e] * s_in;
+                        const float z = __builtin_fmaf(coef, vt[nb][e], xc);
+                        xacc += xc;
+#pragma unroll
+                        for (int o = 0; o < H; ++o) y[o][nb][e] = __builtin_fmaf(mw[o], z, y[o][nb][e]);
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < H; ++j) xin[j] = (j == h) ? xacc : xin[j];
+            }
+        }
+
+        // ---- store Y and the tile's mass partial sums -----------------------------------
+        TY* Yg = static_cast<TY*>(a.Y);
+        float red[16];  // [0, 8): sum of scaled X per head; [8, 16): sum of stored Y
+#pragma unroll
+        for (int o = 0; o < H; ++o) {
+            red[o] = xin[o];
+            red[H + o] = 0.f;
+        }
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+            const int cell = 16 * nb + i16;
+            const long long base =
+                bbase + ((long long)(ty0 + cell / kTileX) * G + tx0 + cell % kTileX) * C + ch0;
+#pragma unroll
+            for (int o = 0; o < H; ++o) {
+                float r[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    r[e] = Store<TY>::round(y[o][nb][e]);
+                    red[H + o] += r[e];
+                }
+                if constexpr (sizeof(TY) == 2)
+                    *reinterpret_cast<uint2*>(Yg + base + o * kD) =
+                        make_uint2(pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3]));
+                else
+                    *reinterpret_cast<float4*>(Yg + base + o * kD) = make_float4(r[0], r[1], r[2], r[3]);
+            }
+        }
+        // Wave sums of the 16 values: the butterfly leaves lane l holding its 16-lane
+        // row's sum of value l & 15; the rows and waves are added in a fixed order.
+        fold_half<8, 0x140>(red, lane, 3);  // row_mirror: partner l ^ 15
+        fold_half<4, 0x141>(red, lane, 2);  // row_half_mirror: partner l ^ 7
+        fold_half<2, 0x4E>(red, lane, 1);   // quad_perm [2,3,0,1]: partner l ^ 2
+        fold_half<1, 0xB1>(red, lane, 0);   // quad_perm [1,0,3,2]: partner l ^ 1
+        sR[tid] = red[0];
+        __syncthreads();
+        if (tid < 2 * H) {
+            float sum = 0.f;
+#pragma unroll
+            for (int r = 0; r < kThreads / 16; ++r) sum += sR[r * 16 + tid];
+            const int j = tid % H;
+            float* dst = tid < H ? a.part_in : a.part_out;
+            dst[((long long)b * H + j) * tpb + tile] = sum;
+        }
+        if (t_next < 0) break;
+        t_cur = t_next;
+    }
+}
+
 template <typename T, int D, typename TY>
 hipError_t launch_tdy(const StencilArgs& a, hipStream_t s) {
     using L = Layout<T, D>;
@@ -529,9 +942,27 @@ hipError_t launch_tdy(const StencilArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
+template <typename TY>
+hipError_t launch_mfma(const StencilArgs& a, hipStream_t s) {
+    static int n_cu = 0;
+    if (!n_cu) {
+        int dev = 0;
+        hipError_t e = hipGetDevice(&dev);
+        if (e == hipSuccess) e = hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e != hipSuccess) return e;
+    }
+    const int tiles = a.B * (a.G / kTileY) * (a.G / kTileX);
+    const int grid = tiles < 2 * n_cu ? tiles : 2 * n_cu;  // two persistent workgroups per CU
+    hipLaunchKernelGGL((stencil_mfma_kernel<TY>), dim3(grid), dim3(mf::kThreads), 0, s, a);
+    return hipGetLastError();
+}
+
 template <typename T, int D>
 hipError_t launch_td(const StencilArgs& a, hipStream_t s) {
-    return a.y_f32 ? launch_tdy<T, D, float>(a, s) : launch_tdy<T, D, T>(a, s);
+    if constexpr (sizeof(T) == 2 && D == 64)
+        return a.y_f32 ? launch_mfma<float>(a, s) : launch_mfma<bf16_t>(a, s);
+    else
+        return a.y_f32 ? launch_tdy<T, D, float>(a, s) : launch_tdy<T, D, T>(a, s);
 }
 
 template <typename T>
