@@ -81,50 +81,11 @@ __device__ __forceinline__ void store_tile_f32(f32x16 (&acc)[4][4], float* obase
 }
 constexpr int kStoresF32 = 64;  // global stores per wave per tile (fp32 epilogue)
 
-// bf16 epilogue through LDS: for each 32-row block j and each half of the
-// wave's 128 columns, the wave writes its accumulators (MFMA layout, 8-byte
-// pieces) into a private LDS region and reads them back row-contiguous, so one
-// store instruction writes eight whole 128-byte row segments. Rows are padded
-// to 144 bytes: the 8-byte writes of 16 consecutive rows hit distinct banks.
+// Rows of the per-wave staging region are padded to 144 bytes: the 8-byte writes
+// of 16 consecutive rows hit distinct banks.
 constexpr int kEpiRowB = 144;
 constexpr int kEpiWaveB = 32 * kEpiRowB;
 constexpr int kStoresBf16 = 32;  // global stores per wave per tile (bf16 epilogue)
-
-template <int kAct>
-__device__ __forceinline__ void store_tile_bf16(f32x16 (&acc)[4][4], bf16_t* obase, int ncol,
-                                                unsigned char* ep, int lane) {
-    const int r32 = lane & 31, half = lane >> 5;
-    unsigned char* wp = ep + r32 * kEpiRowB + half * 8;
-    const unsigned char* rp = ep + (lane >> 3) * kEpiRowB + (lane & 7) * 16;
-    const unsigned gl = (unsigned)(((lane >> 3) * ncol + (lane & 7) * 8) * 2);
-    char* ob = reinterpret_cast<char*>(obase);
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            pin_acc(acc[2 * p][j]);
-            pin_acc(acc[2 * p + 1][j]);
-#pragma unroll
-            for (int ii = 0; ii < 2; ++ii)
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int i = 2 * p + ii;
-                    const uint2 v = make_uint2(
-                        pack_bf16x2(act_of<kAct>(acc[i][j][4 * q + 0]), act_of<kAct>(acc[i][j][4 * q + 1])),
-                        pack_bf16x2(act_of<kAct>(acc[i][j][4 * q + 2]), act_of<kAct>(acc[i][j][4 * q + 3])));
-                    *reinterpret_cast<uint2*>(wp + (ii * 32 + 8 * q) * 2) = v;
-                }
-#pragma unroll
-            for (int s4 = 0; s4 < 4; ++s4) {
-                const uint4 v = *reinterpret_cast<const uint4*>(rp + s4 * 8 * kEpiRowB);
-                const long long uoff = ((long long)(j * 32 + s4 * 8) * ncol + p * 64) * 2;  // uniform
-                *reinterpret_cast<uint4*>(ob + uoff + gl) = v;
-            }
-            // One 32-row x 64-column block at a time: converting the whole tile up
-            // front would need 256 more registers.
-            __builtin_amdgcn_sched_barrier(0);
-        }
-}
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
@@ -333,6 +294,79 @@ __device__ __forceinline__ void slab_group(const Walk& wk, int kb, int wave, uns
     slab_step<T, 3, false, !kLast>(wk, kb + 3, wave, lds, fb, acc, f, y);
 }
 
+// ---- bf16 epilogue ------------------------------------------------------------------
+// The tile is first converted (activation, bf16) into registers, 4 consecutive
+// channels per piece; it then leaves through a per-wave LDS staging region one
+// group (32 rows x 64 columns) at a time -- written in the MFMA layout, read back
+// row-contiguous -- so each store writes eight whole 128-byte row segments. Two
+// groups are in flight: group g+1 is staged while group g's read-back lands.
+struct OutBuf {
+    uint2 v[8][8];  // [group 2j + p][4 ii + q]: 4 consecutive channels, bf16
+};
+
+template <int kAct>
+__device__ __forceinline__ void convert_tile(f32x16 (&acc)[4][4], OutBuf& ob) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            pin_acc(acc[2 * p][j]);
+            pin_acc(acc[2 * p + 1][j]);
+#pragma unroll
+            for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int i = 2 * p + ii;
+                    ob.v[2 * j + p][4 * ii + q] = make_uint2(
+                        pack_bf16x2(act_of<kAct>(acc[i][j][4 * q + 0]), act_of<kAct>(acc[i][j][4 * q + 1])),
+                        pack_bf16x2(act_of<kAct>(acc[i][j][4 * q + 2]), act_of<kAct>(acc[i][j][4 * q + 3])));
+                }
+        }
+}
+
+// Staging of one group: lane (row r32 = lane % 32, half = lane / 32) writes its 8
+// pieces of 4 channels; read back, lane l takes 16 bytes of row l/8 (+8 s4).
+template <int Gr>
+__device__ __forceinline__ void stage_write(const OutBuf& ob, unsigned char* wp) {
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            *reinterpret_cast<uint2*>(wp + (ii * 32 + 8 * q) * 2) = ob.v[Gr][4 * ii + q];
+}
+__device__ __forceinline__ void stage_read(const unsigned char* rp, uint4 (&tmp)[4]) {
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) tmp[s4] = *reinterpret_cast<const uint4*>(rp + s4 * 8 * kEpiRowB);
+}
+template <int Gr>
+__device__ __forceinline__ void store_group(char* ob, unsigned gl, int ncol, const uint4 (&tmp)[4]) {
+    constexpr int j = Gr >> 1, p = Gr & 1;
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) {
+        const long long uoff = ((long long)(j * 32 + s4 * 8) * ncol + p * 64) * 2;  // uniform
+        __builtin_nontemporal_store(__builtin_bit_cast(u32x4, tmp[s4]),
+                                    reinterpret_cast<u32x4*>(ob + uoff + gl));
+    }
+}
+
+template <int kAct>
+__device__ __forceinline__ void store_tile_bf16(f32x16 (&acc)[4][4], char* ob, int ncol,
+                                                unsigned char* ep_w, const unsigned char* ep_r,
+                                                unsigned gl) {
+    OutBuf obuf;
+    convert_tile<kAct>(acc, obuf);
+    uint4 t[2][4];
+    stage_write<0>(obuf, ep_w);
+    stage_read(ep_r, t[0]);
+    static_for<1, 8>([&](auto gc) {
+        constexpr int Gr = decltype(gc)::value;
+        stage_write<Gr>(obuf, ep_w);  // LDS keeps each wave's order: after read Gr-1
+        stage_read(ep_r, t[Gr & 1]);
+        store_group<Gr - 1>(ob, gl, ncol, t[(Gr - 1) & 1]);
+    });
+    store_group<7>(ob, gl, ncol, t[1]);
+}
+
 template <typename T>
 __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs g) {
     __shared__ __attribute__((aligned(1024))) unsigned char lds[4 * kStageB];
@@ -394,6 +428,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs g) {
 
     bool stores_pending = false;  // the previous tile's stores follow slabs 0..3 of this one
     f32x16 acc[4][4];
+    unsigned char* ep_w = epi + wave * kEpiWaveB + r32 * kEpiRowB + half * 8;
+    const unsigned char* ep_r = epi + wave * kEpiWaveB + (lane >> 3) * kEpiRowB + (lane & 7) * 16;
+    const unsigned ep_gl = (unsigned)(((lane >> 3) * g.ncol + (lane & 7) * 8) * 2);
     while (true) {
         wk.next = wk.tile + wk.stride < wk.tile_end ? wk.tile + wk.stride : -1;
         if (wk.next >= 0) tile_rows<T>(g, wk.next, wk.nN, &wk.x_nxt, &wk.w_nxt);
@@ -418,22 +455,22 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs g) {
         const int col0 = n0 - plane * g.ncol + wn * 128;
         // The whole 256-wide N tile lies in one output plane: uniform activation.
         if constexpr (kBf16) {
-            unsigned char* ep = epi + wave * kEpiWaveB;
-            bf16_t* obase = reinterpret_cast<bf16_t*>(out) + (long long)(m0 + wm * 128) * g.ncol + col0;
+            char* obase = reinterpret_cast<char*>(reinterpret_cast<bf16_t*>(out) +
+                                                  (long long)(m0 + wm * 128) * g.ncol + col0);
             // The distinct markers keep the compiler from hoisting the accumulator
             // reads common to the three arms above the switch (all 256 at once).
             switch (g.act[plane]) {
                 case 1:
                     asm volatile("; epilogue relu");
-                    store_tile_bf16<1>(acc, obase, g.ncol, ep, lane);
+                    store_tile_bf16<1>(acc, obase, g.ncol, ep_w, ep_r, ep_gl);
                     break;
                 case 2:
                     asm volatile("; epilogue gelu");
-                    store_tile_bf16<2>(acc, obase, g.ncol, ep, lane);
+                    store_tile_bf16<2>(acc, obase, g.ncol, ep_w, ep_r, ep_gl);
                     break;
                 default:
                     asm volatile("; epilogue identity");
-                    store_tile_bf16<0>(acc, obase, g.ncol, ep, lane);
+                    store_tile_bf16<0>(acc, obase, g.ncol, ep_w, ep_r, ep_gl);
                     break;
             }
         } else {
