@@ -15,6 +15,7 @@ typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_v;
 typedef __attribute__((ext_vector_type(16))) float f32x16;
 typedef __attribute__((ext_vector_type(4))) float f32x4;
 typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
+typedef __attribute__((ext_vector_type(2))) unsigned int u32x2;
 
 constexpr int kWave = 64;
 

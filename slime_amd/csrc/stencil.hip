@@ -26,6 +26,7 @@
 #include "common.hpp"
 #include "kernels.hpp"
 
+#include <cstring>
 #include <type_traits>
 
 namespace slime {
@@ -481,16 +482,20 @@ __global__ __launch_bounds__((Layout<T, D>::kThreads), 2) void stencil_kernel(St
 //   U^T  = X_halo^T . Kmat^T      Kmat[cell][n] = K[h][k] if halo row n = n_k(cell)
 //   Vt^T = V_halo^T . Att^T       Att[cell][n]  = a_k(cell) likewise (0 elsewhere)
 // (M = 16 channels, N = 16 cells, K = 64 halo rows; v_mfma_f32_16x16x32_bf16).
-// The sparse 32 x 64 weight matrices live in LDS; each head rewrites only their 9
-// non-zeros per cell. Weights enter as bf16 hi + lo pairs (w = hi + lo to 2^-17
-// relative) and X, V are bf16 already, so every product is exact in fp32 and the
-// sums keep fp32 accuracy. The halo^T operands come straight from the row-major
-// halo through ds_read_b64_tr_b16 (gfx950's transposing LDS read).
+// Weights enter as bf16 hi + lo pairs (w = hi + lo to 2^-17 relative) and X, V
+// are bf16 already, so every product is exact in fp32 and the sums keep fp32
+// accuracy. The halo^T operands come straight from the row-major halo through
+// ds_read_b64_tr_b16 (gfx950's transposing LDS read). Kmat depends only on the
+// pod, the head and the tile geometry, so it is built once on the host
+// (fill_stencil_kmat) and read from L2; Att is built per head.
 //
-// Per head: each wave computes 16 cells x 32 halo rows of the scores <P, I> on the
-// matrix cores and keeps the 9 per cell that are neighbours; all lanes run the
-// softmax (8 per cell) and write the weights; each wave then owns 16 channels of
-// all 32 cells for growth, update and head mixing in registers.
+// Work split: wave w owns cell block cb = w/2 (tile rows 2cb, 2cb+1: 16 cells)
+// and channel half w%2 (32 channels). Each wave computes the scores <P, I> of its
+// 16 cells against the 48 halo rows that can hold their neighbours (matrix
+// cores), keeps the 9 per cell, runs the softmax (4 lanes per cell) and writes
+// Att for its cells into its own LDS region -- nothing crosses waves inside a
+// head, so the only barrier per head is the one that publishes the staged halo.
+// Growth, update and head mixing then run in registers for its 16 x 32 outputs.
 //
 // The kernel is persistent: a workgroup walks a run of tiles (XCD-contiguous), and
 // the staging pipeline runs across tile boundaries -- head 0 of the next tile and
@@ -505,12 +510,14 @@ constexpr int kWaves = kThreads / 64;
 constexpr int offX = 0, offV = kHaloPad * kRowB, offI = 2 * kHaloPad * kRowB,
               offP = 3 * kHaloPad * kRowB;
 constexpr int kBufB = (3 * kHaloPad + kTileCells) * kRowB;  // 28 KiB
-constexpr int kMatB = kTileCells * kRowB;                    // one 32 x 64 bf16 weight matrix
-constexpr int kS9 = 12;                                      // floats per cell in the score buffer
-// Per-tile parameter block (fp32): K[8][9], M[8][8] (M[o][h] at o*8+h), mu[8],
-// sigma[8], scale[8]; then, for per-cell growth, mu and sigma [cell][8].
-constexpr int kPK = 0, kPM = 72, kPMu = 136, kPSg = 144, kPSc = 152, kPScal = 160;
-constexpr int kPCellMu = 160, kPCellSg = 160 + kTileCells * 8, kParF = 160 + 2 * kTileCells * 8;
+constexpr int kWC = 16;                                     // cells per wave
+constexpr int kAttB = kWC * kRowB;                          // one 16 x 64 bf16 matrix
+constexpr int kS9 = 12;  // floats per cell in a score buffer (9 used, 9..11 take discards)
+constexpr int kKmatHead = 2 * kTileCells * kRowB;           // hi + lo, 8 KiB per (pod, head)
+// Per-tile parameter block (fp32): M[8][8] (M[o][h] at o*8+h), mu[8], sigma[8],
+// scale[8]; then, for per-cell growth, mu and sigma [cell][8].
+constexpr int kPM = 0, kPMu = 64, kPSg = 72, kPSc = 80, kPScal = 88;
+constexpr int kPCellMu = 88, kPCellSg = 88 + kTileCells * 8, kParF = 88 + 2 * kTileCells * 8;
 
 // 16-byte chunk swizzles inside a 128-byte row. X and V: any four consecutive
 // rows 4j..4j+3, and rows {r, r+2, r+8, r+10}, occupy disjoint chunk pairs, so
@@ -556,6 +563,11 @@ __device__ __forceinline__ void fold_half(float (&v)[16], int lane, int bit) {
     }
 }
 
+// Halo row of neighbour k of tile cell c (4 x 8 tile, 6 x 10 halo).
+__host__ __device__ constexpr int nb_row(int c, int k) {
+    return (c / kTileX + k / 3) * kHaloX + c % kTileX + k % 3;
+}
+
 }  // namespace mf
 
 template <typename TY>
@@ -565,10 +577,10 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
     constexpr int C = H * kD;
     __shared__ __attribute__((aligned(16))) unsigned char bufA[kBufB];
     __shared__ __attribute__((aligned(16))) unsigned char bufB[kBufB];
-    // Weight matrices [cell][halo row] bf16, chunk-swizzled by cell & 7:
-    // 0 = K hi, 1 = K lo, 2 = a hi, 3 = a lo.
-    __shared__ __attribute__((aligned(16))) unsigned char sW[4 * kMatB];
-    __shared__ __attribute__((aligned(16))) float sS9[kTileCells * kS9 + kThreads];  // + discard slots
+    // Per wave: Att of its 16 cells, [hi/lo][cell][halo row] bf16, chunk-swizzled
+    // by cell & 7; and its 16 cells' 9 scores.
+    __shared__ __attribute__((aligned(16))) unsigned char sAtt[kWaves * 2 * kAttB];
+    __shared__ __attribute__((aligned(16))) float sS9[kWaves * kWC * kS9];
     // One parameter block: a tile's block is written after the barrier that ends
     // the previous tile's last head, its last reader.
     __shared__ __attribute__((aligned(16))) float sPar[kParF];
@@ -596,12 +608,19 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
     }
     if (t_cur >= t_end) return;
 
+    const int cb = wave >> 1, chh = wave & 1;   // cell block, channel half
+    const int grp = lane >> 4, i16 = lane & 15;
+    const int cell = kWC * cb + i16;            // this lane's cell in phase B
+    const char* kmat = static_cast<const char*>(a.kmat);
+
     // ---- staging: 8 halo rows (or P rows) per direct-load instruction -------------------
     // Lane l of an instruction lands at row g*8 + l/8, physical chunk l%8, and fetches
     // the logical chunk the row's swizzle maps there. Wave w issues groups w and w+4
-    // of each halo array and group w of the P tile.
+    // of each halo array and group w of the P tile. With the staging, each lane
+    // fetches its Kmat operands (cell, halo rows 32 ks + 8 grp .. +7, hi and lo).
     unsigned boff_xv[2], boff_i[2], boff_p;
     const char *srcX, *srcV, *srcI, *srcP;
+    int pod_nxt = 0;
     auto set_tile = [&](int t) {  // per-lane offsets and bases of tile t
         const int b = t / tpb, tile = t % tpb;
         const int ty0 = (tile / tiles_x) * kTileY, tx0 = (tile % tiles_x) * kTileX;
@@ -623,7 +642,9 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
         srcV = reinterpret_cast<const char*>(static_cast<const bf16_t*>(a.V) + bb);
         srcI = reinterpret_cast<const char*>(static_cast<const bf16_t*>(a.I) + bb);
         srcP = reinterpret_cast<const char*>(static_cast<const bf16_t*>(a.P) + bb);
+        pod_nxt = b / a.per_pod;
     };
+    uint4 kq[2][2], kq_nxt[2][2];  // Kmat^T operands [ks][hi/lo]
     auto issue_head = [&](int h, unsigned char* buf) {
         const unsigned hb = (unsigned)(h * kRowB);
         const unsigned lb = lds_addr(buf);
@@ -635,6 +656,12 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
             dma16_saddr(srcI, boff_i[k] + hb, row + offI);
         }
         dma16_saddr(srcP, boff_p + hb, lb + offP + wave * 1024);
+        const char* km = kmat + (long long)(pod_nxt * H + h) * kKmatHead + cell * kRowB + 16 * grp;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int m = 0; m < 2; ++m)
+                kq_nxt[ks][m] = *reinterpret_cast<const uint4*>(km + m * (kTileCells * kRowB) + 64 * ks);
     };
     // Per-tile parameters: up to three floats per lane, loaded into registers with
     // the tile's first staging and written to LDS once they have landed.
@@ -643,8 +670,7 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
         const int b = t / tpb, tile = t % tpb;
         const int pod = b / a.per_pod;
         pre[0] = pre[1] = pre[2] = 0.f;
-        if (tid < kPK + 72) pre[0] = a.K[pod * 72 + tid];
-        else if (tid < kPM + 64) pre[0] = a.M[pod * 64 + tid - kPM];
+        if (tid < kPM + 64) pre[0] = a.M[pod * 64 + tid - kPM];
         else if (tid < kPSg + 8) {
             if (!a.per_cell) pre[0] = tid < kPSg ? a.mu[pod * 8 + tid - kPMu] : a.sigma[pod * 8 + tid - kPSg];
         } else if (tid < kPScal) {
@@ -652,9 +678,9 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
         }
         if (a.per_cell) {
             const int ty0 = (tile / tiles_x) * kTileY, tx0 = (tile % tiles_x) * kTileX;
-            const int cell = tid >> 3, hh = tid & 7;
+            const int pcell = tid >> 3, hh = tid & 7;
             const long long pi =
-                (((long long)pod * G + ty0 + cell / kTileX) * G + tx0 + cell % kTileX) * H + hh;
+                (((long long)pod * G + ty0 + pcell / kTileX) * G + tx0 + pcell % kTileX) * H + hh;
             pre[1] = a.mu[pi];
             pre[2] = a.sigma[pi];
         }
@@ -667,75 +693,73 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
         }
     };
 
-    // The weight matrices are zero except at the 9 neighbours of each cell.
-    for (int i = tid; i < 4 * kMatB / 16; i += kThreads)
-        reinterpret_cast<uint4*>(sW)[i] = make_uint4(0u, 0u, 0u, 0u);
+    // Att is zero except at the 9 neighbours of each cell.
+    for (int i = tid; i < kWaves * 2 * kAttB / 16; i += kThreads)
+        reinterpret_cast<uint4*>(sAtt)[i] = make_uint4(0u, 0u, 0u, 0u);
     set_tile(t_cur);
     fetch_params(t_cur);
     issue_head(0, bufA);
 
     // ---- per-lane roles (tile independent) ----------------------------------------------
-    const int grp = lane >> 4, i16 = lane & 15;
-    // softmax: cell sc, neighbour sj (lane sj == 0 also takes neighbour 8)
-    const int sc = tid >> 3, sj = tid & 7;
-    auto wpos = [&](int k) {  // byte offset of (cell sc, neighbour k) in a weight matrix
-        const int scy = sc / kTileX, scx = sc % kTileX;
-        const int n = (scy + k / 3) * kHaloX + scx + k % 3;
-        return sc * kRowB + (((n >> 3) ^ (sc & 7)) << 4) + (n & 7) * 2;
-    };
-    const int wp_j = wpos(sj), wp_8 = wpos(8);
-    // scores: this wave's 16 cells (block cb) x 32 halo rows (block hb), as two
-    // 16 x 16 blocks j; A = P rows, B = I rows, K = channels.
-    const int cb = wave >> 1, hb = wave & 1;
-    unsigned sp_off[2], si_off[2][2], s9_off[2][4];
+    unsigned char* att = sAtt + wave * 2 * kAttB;
+    float* s9 = sS9 + wave * kWC * kS9;
+    // scores: A = P rows of cells 16 cb + i16, B = I rows of halo blocks j = cb .. cb+2
+    // (the 48 halo rows holding the block's neighbours); K = channels.
+    unsigned sp_off[2], si_off[3][2], s9_off[3][4];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-        const int cell = 16 * cb + i16;
         sp_off[ks] = (unsigned)(offP + cell * kRowB + (((4 * ks + grp) ^ swz_ip(cell)) << 4));
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int n = 32 * hb + 16 * j + i16;
-            si_off[j][ks] = (unsigned)(offI + n * kRowB + (((4 * ks + grp) ^ swz_ip(n)) << 4));
+        for (int jj = 0; jj < 3; ++jj) {
+            const int n = 16 * (cb + jj) + i16;
+            si_off[jj][ks] = (unsigned)(offI + n * kRowB + (((4 * ks + grp) ^ swz_ip(n)) << 4));
         }
     }
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int jj = 0; jj < 3; ++jj)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            // result (j, e): cell 16 cb + 4 grp + e, halo row n = 32 hb + 16 j + i16
-            const int cell = 16 * cb + 4 * grp + e, n = 32 * hb + 16 * j + i16;
-            const int dy = n / kHaloX - cell / kTileX, dx = n % kHaloX - cell % kTileX;
+            // result (jj, e): cell kWC cb + 4 grp + e, halo row n = 16 (cb + jj) + i16
+            const int lc = 4 * grp + e, c = kWC * cb + lc, n = 16 * (cb + jj) + i16;
+            const int dy = n / kHaloX - c / kTileX, dx = n % kHaloX - c % kTileX;
             const bool keep = n < kHaloCells && (unsigned)dy < 3u && (unsigned)dx < 3u;
-            s9_off[j][e] = (unsigned)(keep ? cell * kS9 + 3 * dy + dx : kTileCells * kS9 + tid) * 4u;
+            s9_off[jj][e] = (unsigned)(lc * kS9 + (keep ? 3 * dy + dx : 9 + jj)) * 4u;
         }
-    // phase B: channels 16 wave + 4 grp .. +3 of cells 16 nb + i16.
-    const int ch0 = 16 * wave + 4 * grp;
-    unsigned tr_off[2][2];  // halo row 32 ks + 8 grp + 4 hf + i16/4, channels 16 wave + 4 (i16 % 4)
+    // softmax: 4 lanes per cell; lane q of cell sc takes neighbours q and q + 4,
+    // lane 0 also neighbour 8.
+    const int sc = lane >> 2, sq = lane & 3;
+    auto wpos = [&](int k) {  // byte offset of (cell sc, neighbour k) in an Att matrix
+        const int n = nb_row(kWC * cb + sc, k);
+        return sc * kRowB + (((n >> 3) ^ (sc & 7)) << 4) + (n & 7) * 2;
+    };
+    const int wp_a = wpos(sq), wp_b = wpos(sq + 4), wp_8 = wpos(8);
+    // phase B: channels 32 chh + 16 mb + 4 grp .. +3 (mb = 0, 1) of cell `cell`.
+    unsigned tr_off[2][2][2];  // [mb][ks][hf]: halo row 32 ks + 8 grp + 4 hf + i16/4
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
+    for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-            const int row = 32 * ks + 8 * grp + 4 * hf + (i16 >> 2);
-            const int q = i16 & 3;
-            tr_off[ks][hf] = (unsigned)(row * kRowB + (((2 * wave + (q >> 1)) ^ swz_xv(row)) << 4) +
-                                        8 * (q & 1));
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                const int row = 32 * ks + 8 * grp + 4 * hf + (i16 >> 2);
+                const int cblk = 2 * chh + mb, q = i16 & 3;
+                tr_off[mb][ks][hf] = (unsigned)(row * kRowB + (((2 * cblk + (q >> 1)) ^ swz_xv(row)) << 4) +
+                                                8 * (q & 1));
+            }
+    unsigned at_off[2];  // Att^T operand: local cell i16, halo rows 32 ks + 8 grp .. +7
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) at_off[ks] = (unsigned)(i16 * kRowB + (((4 * ks + grp) ^ (i16 & 7)) << 4));
+    unsigned xc_off[2];  // centre row of `cell`, channels 32 chh + 16 mb + 4 grp .. +3
+    {
+        const int crow = nb_row(cell, 4);
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) {
+            const int cblk = 2 * chh + mb;
+            xc_off[mb] = (unsigned)(offX + crow * kRowB + (((2 * cblk + (grp >> 1)) ^ swz_xv(crow)) << 4) +
+                                    8 * (grp & 1));
         }
-    unsigned w_off[2][2];  // cell 16 nb + i16, halo rows 32 ks + 8 grp .. +7
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            const int cell = 16 * nb + i16;
-            w_off[nb][ks] = (unsigned)(cell * kRowB + (((4 * ks + grp) ^ (cell & 7)) << 4));
-        }
-    unsigned xc_off[2];  // centre row of cell 16 nb + i16, channels ch0 .. ch0+3
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-        const int cell = 16 * nb + i16;
-        const int crow = (cell / kTileX + 1) * kHaloX + cell % kTileX + 1;
-        xc_off[nb] = (unsigned)(offX + crow * kRowB + (((2 * wave + (grp >> 1)) ^ swz_xv(crow)) << 4) +
-                                8 * (grp & 1));
     }
+    const int ch0 = 32 * chh + 4 * grp;  // + 16 mb: this lane's output channels
 
     constexpr float kLog2e = 1.4426950408889634f;
     const float score_scale = kLog2e / 8.0f;  // log2(e) / sqrt(D)
@@ -755,9 +779,9 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
         for (int o = 0; o < H; ++o) {
             xin[o] = 0.f;
 #pragma unroll
-            for (int nb = 0; nb < 2; ++nb)
+            for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) y[o][nb][e] = 0.f;
+                for (int e = 0; e < 4; ++e) y[o][mb][e] = 0.f;
         }
 
         for (int h = 0; h < H; ++h, ++gh) {
@@ -765,6 +789,10 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
             unsigned char* nxt = (gh & 1) ? bufA : bufB;
             wait_vm0();       // this wave's loads of head h have landed
             __syncthreads();  // ... and every other wave's; head h-1 is fully consumed
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                for (int m = 0; m < 2; ++m) kq[ks][m] = kq_nxt[ks][m];
             if (h == 0) store_params(par);
             if (h + 1 < H) {
                 issue_head(h + 1, nxt);
@@ -774,110 +802,97 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
                 issue_head(0, nxt);
             }
 
-            // ---- S4 scores: S[cell][n] = <P_cell, I_n>, kept for the 9 neighbours --------
+            // ---- S4 scores of this wave's cells, kept for the 9 neighbours --------------
             {
                 const uint4 pa0 = *reinterpret_cast<const uint4*>(buf + sp_off[0]);
                 const uint4 pa1 = *reinterpret_cast<const uint4*>(buf + sp_off[1]);
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
+                for (int jj = 0; jj < 3; ++jj) {
                     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-                    acc = mfma16(pa0, *reinterpret_cast<const uint4*>(buf + si_off[j][0]), acc);
-                    acc = mfma16(pa1, *reinterpret_cast<const uint4*>(buf + si_off[j][1]), acc);
+                    acc = mfma16(pa0, *reinterpret_cast<const uint4*>(buf + si_off[jj][0]), acc);
+                    acc = mfma16(pa1, *reinterpret_cast<const uint4*>(buf + si_off[jj][1]), acc);
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
-                        *reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(sS9) + s9_off[j][e]) =
+                        *reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(s9) + s9_off[jj][e]) =
                             acc[e];
                 }
             }
-            lds_barrier();
-
-            // ---- softmax and the weight matrices of this head -----------------------------
+            // ---- softmax; Att of this wave's cells (its own LDS: in order, no barrier) -
             {
-                const float* srow = sS9 + sc * kS9;
-                const float s_j = srow[sj], s_8 = srow[8];
-                const float mx = group_max<8>(sj == 0 ? fmaxf(s_j, s_8) : s_j);
-                const float e_j = exp2_fast((s_j - mx) * score_scale);
+                const float* srow = s9 + sc * kS9;
+                const float s_a = srow[sq], s_b = srow[sq + 4], s_8 = srow[8];
+                const float m_l = sq == 0 ? fmaxf(fmaxf(s_a, s_b), s_8) : fmaxf(s_a, s_b);
+                const float mx = group_max<4>(m_l);
+                const float e_a = exp2_fast((s_a - mx) * score_scale);
+                const float e_b = exp2_fast((s_b - mx) * score_scale);
                 const float e_8 = exp2_fast((s_8 - mx) * score_scale);
-                const float inv = rcp_fast(group_sum<8>(sj == 0 ? e_j + e_8 : e_j));
+                const float inv = rcp_fast(group_sum<4>(sq == 0 ? e_a + e_b + e_8 : e_a + e_b));
                 bf16_t hi, lo;
-                split_bf16(par[kPK + h * 9 + sj], hi, lo);
-                *reinterpret_cast<bf16_t*>(sW + 0 * kMatB + wp_j) = hi;
-                *reinterpret_cast<bf16_t*>(sW + 1 * kMatB + wp_j) = lo;
-                split_bf16(e_j * inv, hi, lo);
-                *reinterpret_cast<bf16_t*>(sW + 2 * kMatB + wp_j) = hi;
-                *reinterpret_cast<bf16_t*>(sW + 3 * kMatB + wp_j) = lo;
-                if (sj == 0) {
-                    split_bf16(par[kPK + h * 9 + 8], hi, lo);
-                    *reinterpret_cast<bf16_t*>(sW + 0 * kMatB + wp_8) = hi;
-                    *reinterpret_cast<bf16_t*>(sW + 1 * kMatB + wp_8) = lo;
+                split_bf16(e_a * inv, hi, lo);
+                *reinterpret_cast<bf16_t*>(att + wp_a) = hi;
+                *reinterpret_cast<bf16_t*>(att + kAttB + wp_a) = lo;
+                split_bf16(e_b * inv, hi, lo);
+                *reinterpret_cast<bf16_t*>(att + wp_b) = hi;
+                *reinterpret_cast<bf16_t*>(att + kAttB + wp_b) = lo;
+                if (sq == 0) {
                     split_bf16(e_8 * inv, hi, lo);
-                    *reinterpret_cast<bf16_t*>(sW + 2 * kMatB + wp_8) = hi;
-                    *reinterpret_cast<bf16_t*>(sW + 3 * kMatB + wp_8) = lo;
+                    *reinterpret_cast<bf16_t*>(att + wp_8) = hi;
+                    *reinterpret_cast<bf16_t*>(att + kAttB + wp_8) = lo;
                 }
             }
-            lds_barrier();
 
             // ---- S2 / S5 on the matrix cores, then S3, S6 and head mixing -----------------
             {
-                uint4 ax[2], av[2];
-#pragma unroll
-                for (int ks = 0; ks < 2; ++ks) {
-                    const uint2 x0 = read_tr16(buf + offX + tr_off[ks][0]);
-                    const uint2 x1 = read_tr16(buf + offX + tr_off[ks][1]);
-                    const uint2 v0 = read_tr16(buf + offV + tr_off[ks][0]);
-                    const uint2 v1 = read_tr16(buf + offV + tr_off[ks][1]);
-                    ax[ks] = make_uint4(x0.x, x0.y, x1.x, x1.y);
-                    av[ks] = make_uint4(v0.x, v0.y, v1.x, v1.y);
-                }
-                f32x4 u[2], vt[2];
-#pragma unroll
-                for (int nb = 0; nb < 2; ++nb) u[nb] = vt[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+                uint4 aw[2][2];  // Att^T [ks][hi/lo]
 #pragma unroll
                 for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-                    for (int m = 0; m < 2; ++m)  // hi, lo
+                    for (int m = 0; m < 2; ++m)
+                        aw[ks][m] = *reinterpret_cast<const uint4*>(att + m * kAttB + at_off[ks]);
+                f32x4 u[2], vt[2];
 #pragma unroll
-                        for (int nb = 0; nb < 2; ++nb) {
-                            u[nb] = mfma16(ax[ks], *reinterpret_cast<const uint4*>(sW + m * kMatB + w_off[nb][ks]),
-                                           u[nb]);
-                            vt[nb] = mfma16(av[ks],
-                                            *reinterpret_cast<const uint4*>(sW + (2 + m) * kMatB + w_off[nb][ks]),
-                                            vt[nb]);
+                for (int mb = 0; mb < 2; ++mb) {
+                    u[mb] = vt[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int ks = 0; ks < 2; ++ks) {
+                        const uint2 x0 = read_tr16(buf + offX + tr_off[mb][ks][0]);
+                        const uint2 x1 = read_tr16(buf + offX + tr_off[mb][ks][1]);
+                        const uint2 v0 = read_tr16(buf + offV + tr_off[mb][ks][0]);
+                        const uint2 v1 = read_tr16(buf + offV + tr_off[mb][ks][1]);
+                        const uint4 ax = make_uint4(x0.x, x0.y, x1.x, x1.y);
+                        const uint4 av = make_uint4(v0.x, v0.y, v1.x, v1.y);
+#pragma unroll
+                        for (int m = 0; m < 2; ++m) {
+                            u[mb] = mfma16(ax, kq[ks][m], u[mb]);
+                            vt[mb] = mfma16(av, aw[ks][m], vt[mb]);
                         }
+                    }
+                }
                 const float s_in = par[kPSc + h];  // deferred mass scale of X
                 const float two_dt = 2.0f * dt;
                 float mw[H];
 #pragma unroll
                 for (int o = 0; o < H; ++o) mw[o] = par[kPM + o * H + h];
-                float ga[2], gb[2];  // (U s - mu) / (sigma + 1e-7) * sqrt(log2 e) = U ga - gb
-                if (a.per_cell) {
-#pragma unroll
-                    for (int nb = 0; nb < 2; ++nb) {
-                        const int cell = 16 * nb + i16;
-                        const float g = sqrt_log2e / (par[kPCellSg + cell * 8 + h] + 1e-7f);
-                        ga[nb] = g * s_in;
-                        gb[nb] = par[kPCellMu + cell * 8 + h] * g;
-                    }
-                } else {
-                    const float g = sqrt_log2e / (par[kPSg + h] + 1e-7f);
-                    ga[0] = ga[1] = g * s_in;
-                    gb[0] = gb[1] = par[kPMu + h] * g;
-                }
+                // (U s - mu) / (sigma + 1e-7) * sqrt(log2 e) = U ga - gb
+                const float mu_h = a.per_cell ? par[kPCellMu + cell * 8 + h] : par[kPMu + h];
+                const float sg_h = a.per_cell ? par[kPCellSg + cell * 8 + h] : par[kPSg + h];
+                const float gsc = sqrt_log2e / (sg_h + 1e-7f);
+                const float ga = gsc * s_in, gb = mu_h * gsc;
                 float xacc = 0.f;
 #pragma unroll
-                for (int nb = 0; nb < 2; ++nb) {
-                    const uint2 xr = *reinterpret_cast<const uint2*>(buf + xc_off[nb]);
+                for (int mb = 0; mb < 2; ++mb) {
+                    const uint2 xr = *reinterpret_cast<const uint2*>(buf + xc_off[mb]);
                     const float xv[4] = {bf16lo(xr.x), bf16hi(xr.x), bf16lo(xr.y), bf16hi(xr.y)};
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        const float tg = __builtin_fmaf(u[nb][e], ga[nb], -gb[nb]);
+                        const float tg = __builtin_fmaf(u[mb][e], ga, -gb);
                         const float ex = exp2_fast(-tg * tg);
                         const float coef = __builtin_fmaf(ex, two_dt, -dt);  // dt * g
                         const float xc = xv[e] * s_in;
-                        const float z = __builtin_fmaf(coef, vt[nb][e], xc);
+                        const float z = __builtin_fmaf(coef, vt[mb][e], xc);
                         xacc += xc;
 #pragma unroll
-                        for (int o = 0; o < H; ++o) y[o][nb][e] = __builtin_fmaf(mw[o], z, y[o][nb][e]);
+                        for (int o = 0; o < H; ++o) y[o][mb][e] = __builtin_fmaf(mw[o], z, y[o][mb][e]);
                     }
                 }
 #pragma unroll
@@ -893,25 +908,27 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
             red[o] = xin[o];
             red[H + o] = 0.f;
         }
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb) {
-            const int cell = 16 * nb + i16;
+        {
             const long long base =
                 bbase + ((long long)(ty0 + cell / kTileX) * G + tx0 + cell % kTileX) * C + ch0;
 #pragma unroll
-            for (int o = 0; o < H; ++o) {
-                float r[4];
+            for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    r[e] = Store<TY>::round(y[o][nb][e]);
-                    red[H + o] += r[e];
+                for (int o = 0; o < H; ++o) {
+                    float r[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        r[e] = Store<TY>::round(y[o][mb][e]);
+                        red[H + o] += r[e];
+                    }
+                    TY* dst = Yg + base + o * kD + 16 * mb;
+                    // 32-byte pieces per cell: plain stores, so L2 merges the pieces of
+                    // each 128-byte line before it is written back.
+                    if constexpr (sizeof(TY) == 2)
+                        *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3]));
+                    else
+                        *reinterpret_cast<float4*>(dst) = make_float4(r[0], r[1], r[2], r[3]);
                 }
-                if constexpr (sizeof(TY) == 2)
-                    *reinterpret_cast<uint2*>(Yg + base + o * kD) =
-                        make_uint2(pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3]));
-                else
-                    *reinterpret_cast<float4*>(Yg + base + o * kD) = make_float4(r[0], r[1], r[2], r[3]);
-            }
         }
         // Wave sums of the 16 values: the butterfly leaves lane l holding its 16-lane
         // row's sum of value l & 15; the rows and waves are added in a fixed order.
@@ -979,6 +996,43 @@ hipError_t launch_t(const StencilArgs& a, hipStream_t s) {
 }  // namespace
 
 int stencil_tiles_per_batch(int G) { return (G / kTileY) * (G / kTileX); }
+
+size_t stencil_kmat_bytes(int pods) { return (size_t)pods * kHeads * mf::kKmatHead; }
+
+namespace {
+// fp32 -> bf16 bits, round to nearest even (finite inputs).
+uint16_t host_bf16(float f) {
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+float host_f32(uint16_t b) {
+    const uint32_t u = (uint32_t)b << 16;
+    float f;
+    std::memcpy(&f, &u, 4);
+    return f;
+}
+}  // namespace
+
+void fill_stencil_kmat(const float* K, int pods, uint16_t* out) {
+    constexpr int kRow = mf::kD;  // halo rows per cell row (64)
+    std::memset(out, 0, stencil_kmat_bytes(pods));
+    for (int p = 0; p < pods; ++p)
+        for (int h = 0; h < kHeads; ++h) {
+            uint16_t* hi = out + (size_t)(p * kHeads + h) * (mf::kKmatHead / 2);
+            uint16_t* lo = hi + kTileCells * kRow;
+            for (int k = 0; k < 9; ++k) {
+                const float w = K[(p * kHeads + h) * 9 + k];
+                const uint16_t wh = host_bf16(w);
+                const uint16_t wl = host_bf16(w - host_f32(wh));
+                for (int c = 0; c < kTileCells; ++c) {
+                    hi[c * kRow + mf::nb_row(c, k)] = wh;
+                    lo[c * kRow + mf::nb_row(c, k)] = wl;
+                }
+            }
+        }
+}
 
 hipError_t launch_stencil(int dtype, const StencilArgs& a, hipStream_t s) {
     return dtype == 1 ? launch_t<bf16_t>(a, s) : launch_t<float>(a, s);
