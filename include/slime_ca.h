@@ -120,6 +120,30 @@ int slime_ca_mass(slime_ca* ca, double* h_mass_in, double* h_mass_out);
 int slime_ca_fitness(slime_ca* ca, const void* x_hist, int T, float* erank, float* coherence,
                      float* fitness, void* stream);
 
+/* Parameter gradients of slime_ca_backward: device fp32 arrays in the layouts of
+ * slime_ca_params (WP, WI, WV [pods][C][C]; K [pods][H][9]; mu, sigma [pods][H]
+ * or [pods][G][G][H]; M [pods][H][H]). Any pointer may be NULL. */
+typedef struct {
+    float* WP;
+    float* WI;
+    float* WV;
+    float* K;
+    float* mu;
+    float* sigma;
+    float* M;
+} slime_ca_grads;
+
+/* One step from x_in (parallel projections) and the gradient of the loss
+ * L = mean((x_out - target)^2) over all B*G*G*C elements,
+ * x_out taken before its storage rounding: grad_x (device fp32 [B][G][G][C])
+ * and, through grads (may be NULL), the parameter gradients. *loss (host, may be
+ * NULL) receives L, which synchronises the stream. No counterpart in the
+ * reference: it declares gradients (gradients_d and update_gradients,
+ * slime/proto/model.cu:7,13) but never computes them. SLIME_EINVAL for chained
+ * projections. */
+int slime_ca_backward(slime_ca* ca, const void* x_in, const void* target, float* grad_x,
+                      const slime_ca_grads* grads, double* loss, void* hip_stream);
+
 /* Jacobi sweeps used by the last slime_ca_fitness call, B*H ints (host copy). */
 int slime_ca_fitness_sweeps(slime_ca* ca, int* h_sweeps);
 

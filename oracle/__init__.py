@@ -69,7 +69,7 @@ def lib():
         _lib = ctypes.CDLL(_LIB_PATH)
         for name in ("oracle_project", "oracle_potential", "oracle_growth", "oracle_attention",
                      "oracle_propagate", "oracle_mix", "oracle_conserve", "oracle_step",
-                     "oracle_gram", "oracle_coherence", "oracle_fitness"):
+                     "oracle_gram", "oracle_coherence", "oracle_fitness", "oracle_step_backward"):
             getattr(_lib, name).restype = ctypes.c_int
         _lib.oracle_jacobi_eigs.restype = ctypes.c_int
         _lib.oracle_effective_rank.restype = ctypes.c_double
@@ -159,6 +159,33 @@ def step(cfg, X, params, n_steps=1):
     _check(lib().oracle_step(ctypes.byref(cfg.c()), _p(X), *[_p(a) for a in arrs], _p(out),
                              ctypes.c_int(n_steps), _p(mi), _p(mo)), "step")
     return out, mi, mo
+
+
+def step_loss(cfg, X, params, T):
+    """Loss mean((step(X) - T)^2) of one step (parallel projections)."""
+    X, T = _f32(X), _f32(T)
+    arrs = [_f32(params[k]) for k in ("WP", "WI", "WV", "K", "mu", "sigma", "M")]
+    loss = ctypes.c_double()
+    null = ctypes.c_void_p()
+    _check(lib().oracle_step_backward(ctypes.byref(cfg.c()), _p(X), *[_p(a) for a in arrs], _p(T),
+                                      ctypes.byref(loss), *([null] * 8)), "step_backward")
+    return loss.value
+
+
+def step_backward(cfg, X, params, T):
+    """Loss of one step and its gradients: returns (loss, grads) with grads keyed
+    X, WP, WI, WV, K, mu, sigma, M (shapes as the inputs)."""
+    X, T = _f32(X), _f32(T)
+    names = ("WP", "WI", "WV", "K", "mu", "sigma", "M")
+    arrs = [_f32(params[k]) for k in names]
+    grads = {"X": np.empty_like(X)}
+    for k, a in zip(names, arrs):
+        grads[k] = np.empty_like(a)
+    loss = ctypes.c_double()
+    _check(lib().oracle_step_backward(ctypes.byref(cfg.c()), _p(X), *[_p(a) for a in arrs], _p(T),
+                                      ctypes.byref(loss), _p(grads["X"]),
+                                      *[_p(grads[k]) for k in names]), "step_backward")
+    return loss.value, grads
 
 
 def gram(cfg, X):

@@ -30,6 +30,10 @@
 //                    slime/core/organism.cu:256-257
 //   E5 fitness       slime/kernels/warp_ca.cu:219
 //   field adapters   slime/core/organism.cu:691-720 and :723-743
+//   backward         no reference source: the reference declares gradients
+//                    (slime/proto/model.cu:7,13) but never computes them. The
+//                    step's chain rule is written out below, stage by stage,
+//                    and pinned by finite differences of this file's forward.
 #include "ca_oracle.h"
 
 #include <algorithm>
@@ -505,6 +509,255 @@ int oracle_fitness(const oracle_ca_cfg* cfg, const float* hist, int T, double* e
         erank[bh] = oracle_effective_rank(sv.data(), D);
         fitness[bh] = erank[bh] * coh[bh];
     }
+    return 0;
+}
+
+// ---- one step with the MSE loss, and its gradient ---------------------------------------
+// L = mean over all elements of (Y' - T)^2, Y' the conserved output of one step
+// (parallel P/I/V projections). With gradient pointers NULL only the loss is
+// computed. Chain rule, per (batch b, cell r, head h, channel c), k over the 9
+// neighbours n_k(r) (all sums below also run over channels where indexed by c):
+//   S7  r_o = A_o/B_o (A_o = sum X_o, B_o = sum Y_o; 1 when |B_o| <= 1e-6)
+//       gY' = 2 (Y' - T)/N,  Q_o = sum gY' Y_o,  gY_o = r_o (gY' - Q_o/B_o),
+//       gX_o += Q_o/B_o                       (both only when the guard passes)
+//   S6  gZ_h = sum_o M[o][h] gY_o,  gM[o][h] += sum gY_o Z_h,  gX += gZ,
+//       gg = dt gZ Vt,  gVt = dt gZ g
+//   S3  t = (U - mu)/(sigma + 1e-7): gU = gg (-4 t e^{-t^2})/(sigma + 1e-7),
+//       gmu += -gU,  gsigma += -gU t
+//   S2  gX(n_k(r)) += K[h][k] gU(r),  gK[h][k] += sum gU(r) X(n_k(r))
+//   S5  gV(n_k(r)) += a_k gVt(r),  ga_k = <gVt(r), V(n_k(r))>
+//   S4  gs_k = a_k (ga_k - sum_j a_j ga_j),  gP(r) += sum_k gs_k I(n_k)/sqrt(D),
+//       gI(n_k(r)) += gs_k P(r)/sqrt(D)
+//   S1  gP~ = gP [P~ > 0],  gI~ = gI GELU'(I~),  gX += gP~ W_P^T + gI~ W_I^T + gV W_V^T,
+//       gW_P += X^T gP~ (per pod), likewise W_I, W_V
+// Scatters are evaluated as gathers (cell q collects from r = q - offset_k).
+namespace {
+
+inline double gelu_tanh_grad(double x) {
+    const double c0 = 0.7978845608028654, c1 = 0.044715;
+    const double th = std::tanh(c0 * (x + c1 * x * x * x));
+    return 0.5 * (1.0 + th) + 0.5 * x * (1.0 - th * th) * c0 * (1.0 + 3.0 * c1 * x * x);
+}
+
+// out[r][k] += sum_n g[r][n] W[pod][k][n]   (gradient of x W through its input)
+void project_back_input(const Dims& d, const double* g, const float* W, double* out) {
+    const int C = d.C;
+    const long rows = (long)d.B * d.cells;
+#pragma omp parallel for schedule(static)
+    for (long r = 0; r < rows; ++r) {
+        const int pod = (int)(r / d.cells) / d.per_pod;
+        const float* w = W + (size_t)pod * C * C;
+        const double* gr = g + (size_t)r * C;
+        double* o = out + (size_t)r * C;
+        for (int k = 0; k < C; ++k) {
+            double acc = 0.0;
+            for (int n = 0; n < C; ++n) acc += gr[n] * (double)w[(size_t)k * C + n];
+            o[k] += acc;
+        }
+    }
+}
+
+// gW[pod][k][n] = sum over the pod's rows r of x[r][k] g[r][n]
+void project_back_weight(const Dims& d, const double* x, const double* g, float* gW) {
+    const int C = d.C;
+    for (int pod = 0; pod < d.pods; ++pod) {
+        const long r0 = (long)pod * d.per_pod * d.cells, r1 = r0 + (long)d.per_pod * d.cells;
+#pragma omp parallel for schedule(static)
+        for (int k = 0; k < C; ++k) {
+            std::vector<double> acc(C, 0.0);
+            for (long r = r0; r < r1; ++r) {
+                const double xk = x[(size_t)r * C + k];
+                const double* gr = g + (size_t)r * C;
+                for (int n = 0; n < C; ++n) acc[n] += xk * gr[n];
+            }
+            for (int n = 0; n < C; ++n) gW[((size_t)pod * C + k) * C + n] = (float)acc[n];
+        }
+    }
+}
+
+}  // namespace
+
+int oracle_step_backward(const oracle_ca_cfg* cfg, const float* X_in, const float* WP,
+                         const float* WI, const float* WV, const float* K, const float* mu,
+                         const float* sigma, const float* M, const float* T, double* loss,
+                         float* gX, float* gWP, float* gWI, float* gWV, float* gK, float* gmu,
+                         float* gsigma, float* gM) {
+    Dims d;
+    if (!dims_of(cfg, &d) || cfg->pvi_chain || !loss) return -1;
+    const int G = d.G, C = d.C, D = d.D, H = d.H;
+    const int per_cell = cfg->growth_per_cell;
+    const double dt = cfg->dt, inv_sqrt_d = 1.0 / std::sqrt((double)D);
+    const size_t n = (size_t)d.B * d.cells * C;
+    const size_t na = (size_t)d.B * d.cells * H * 9;
+    std::vector<double> x = to_d(X_in, n), pt(n), it(n), P(n), I(n), V(n), U(n), g(n), Vt(n), Y(n);
+    std::vector<double> A(na);
+    // forward, keeping the pre-activations
+    project(d, x.data(), WP, 0, pt.data());
+    project(d, x.data(), WI, 0, it.data());
+    project(d, x.data(), WV, 0, V.data());
+    for (size_t i = 0; i < n; ++i) {
+        P[i] = pt[i] > 0.0 ? pt[i] : 0.0;
+        I[i] = gelu_tanh(it[i]);
+    }
+    potential(d, x.data(), K, U.data());
+    growth(d, per_cell, U.data(), mu, sigma, g.data());
+    attention(d, P.data(), I.data(), A.data());
+    propagate(d, A.data(), V.data(), Vt.data());
+    mix(d, dt, x.data(), g.data(), Vt.data(), M, Y.data());
+    // S7 and the loss
+    std::vector<double> rs((size_t)d.B * H), sx((size_t)d.B * H), sy((size_t)d.B * H);
+    std::vector<char> guard((size_t)d.B * H);
+    for (int b = 0; b < d.B; ++b)
+        for (int o = 0; o < H; ++o) {
+            double ax = 0.0, by = 0.0;
+            for (long cell = 0; cell < d.cells; ++cell)
+                for (int c = 0; c < D; ++c) {
+                    const size_t i = ((size_t)b * d.cells + cell) * C + o * D + c;
+                    ax += x[i];
+                    by += Y[i];
+                }
+            const size_t bo = (size_t)b * H + o;
+            guard[bo] = std::fabs(by) > 1e-6;
+            rs[bo] = guard[bo] ? ax / by : 1.0;
+            sx[bo] = ax;
+            sy[bo] = by;
+        }
+    const double N = (double)n;
+    double L = 0.0;
+    for (size_t i = 0; i < n; ++i) {
+        const size_t bo = (i / ((size_t)d.cells * C)) * H + (i % C) / D;
+        const double e = rs[bo] * Y[i] - T[i];
+        L += e * e;
+    }
+    *loss = L / N;
+    if (!gX) return 0;
+
+    // S7 backward
+    std::vector<double> gY(n), gx(n, 0.0);
+    std::vector<double> Q((size_t)d.B * H, 0.0);
+    for (size_t i = 0; i < n; ++i) {
+        const size_t bo = (i / ((size_t)d.cells * C)) * H + (i % C) / D;
+        gY[i] = 2.0 * (rs[bo] * Y[i] - T[i]) / N;  // gY' for now
+        Q[bo] += gY[i] * Y[i];
+    }
+    for (size_t i = 0; i < n; ++i) {
+        const size_t bo = (i / ((size_t)d.cells * C)) * H + (i % C) / D;
+        if (guard[bo]) {
+            gY[i] = rs[bo] * (gY[i] - Q[bo] / sy[bo]);
+            gx[i] += Q[bo] / sy[bo];
+        }
+    }
+    // S6 backward
+    std::vector<double> gZ(n, 0.0), gg(n), gVt(n), gU(n);
+    std::vector<double> gMd((size_t)d.pods * H * H, 0.0);
+    for (long r = 0; r < (long)d.B * d.cells; ++r) {
+        const int pod = (int)(r / d.cells) / d.per_pod;
+        for (int h = 0; h < H; ++h)
+            for (int c = 0; c < D; ++c) {
+                const size_t i = (size_t)r * C + h * D + c;
+                double acc = 0.0;
+                for (int o = 0; o < H; ++o)
+                    acc += (double)M[((size_t)pod * H + o) * H + h] * gY[(size_t)r * C + o * D + c];
+                gZ[i] = acc;
+                const double z = x[i] + dt * g[i] * Vt[i];
+                for (int o = 0; o < H; ++o)
+                    gMd[((size_t)pod * H + o) * H + h] += gY[(size_t)r * C + o * D + c] * z;
+                gx[i] += acc;
+                gg[i] = dt * acc * Vt[i];
+                gVt[i] = dt * acc * g[i];
+            }
+    }
+    // S3 backward
+    const size_t ng = per_cell ? (size_t)d.pods * d.cells * H : (size_t)d.pods * H;
+    std::vector<double> gmud(ng, 0.0), gsgd(ng, 0.0);
+    for (long r = 0; r < (long)d.B * d.cells; ++r) {
+        const int b = (int)(r / d.cells);
+        const long cell = r % d.cells;
+        const int pod = b / d.per_pod;
+        for (int h = 0; h < H; ++h) {
+            const size_t pi = per_cell ? ((size_t)pod * d.cells + cell) * H + h : (size_t)pod * H + h;
+            const double m = mu[pi], sp = (double)sigma[pi] + 1e-7;
+            for (int c = 0; c < D; ++c) {
+                const size_t i = (size_t)r * C + h * D + c;
+                const double t = (U[i] - m) / sp;
+                const double gu = gg[i] * (-4.0 * t * std::exp(-t * t)) / sp;
+                gU[i] = gu;
+                gmud[pi] += -gu;
+                gsgd[pi] += -gu * t;
+            }
+        }
+    }
+    // S2, S5, S4 backward (gathers over the 9 neighbours)
+    std::vector<double> gV(n, 0.0), gP(n, 0.0), gI(n, 0.0), gS(na);
+    std::vector<double> gKd((size_t)d.pods * H * 9, 0.0);
+    for (int b = 0; b < d.B; ++b) {
+        const int pod = b / d.per_pod;
+        for (int y = 0; y < G; ++y)
+            for (int xx = 0; xx < G; ++xx) {
+                const size_t r = ((size_t)b * G + y) * G + xx;
+                for (int h = 0; h < H; ++h) {
+                    const double* a = A.data() + (r * H + h) * 9;
+                    double ga[9], sum = 0.0;
+                    for (int k = 0; k < 9; ++k) {
+                        const int dy = k / 3 - 1, dx = k % 3 - 1;
+                        const size_t q = ((size_t)b * G + wrap(y + dy, G)) * G + wrap(xx + dx, G);
+                        double acc = 0.0, acck = 0.0;
+                        for (int c = 0; c < D; ++c) {
+                            acc += gVt[r * C + h * D + c] * V[q * C + h * D + c];
+                            acck += gU[r * C + h * D + c] * x[q * C + h * D + c];
+                        }
+                        ga[k] = acc;
+                        sum += a[k] * acc;
+                        gKd[((size_t)pod * H + h) * 9 + k] += acck;
+                    }
+                    for (int k = 0; k < 9; ++k) gS[(r * H + h) * 9 + k] = a[k] * (ga[k] - sum);
+                    for (int k = 0; k < 9; ++k) {
+                        const int dy = k / 3 - 1, dx = k % 3 - 1;
+                        const size_t q = ((size_t)b * G + wrap(y + dy, G)) * G + wrap(xx + dx, G);
+                        const double gs = gS[(r * H + h) * 9 + k] * inv_sqrt_d;
+                        for (int c = 0; c < D; ++c) gP[r * C + h * D + c] += gs * I[q * C + h * D + c];
+                    }
+                }
+            }
+    }
+    for (int b = 0; b < d.B; ++b) {
+        const int pod = b / d.per_pod;
+        for (int y = 0; y < G; ++y)
+            for (int xx = 0; xx < G; ++xx) {
+                const size_t q = ((size_t)b * G + y) * G + xx;
+                for (int k = 0; k < 9; ++k) {
+                    const int dy = k / 3 - 1, dx = k % 3 - 1;
+                    const size_t r = ((size_t)b * G + wrap(y - dy, G)) * G + wrap(xx - dx, G);
+                    for (int h = 0; h < H; ++h) {
+                        const double a = A[(r * H + h) * 9 + k];
+                        const double gs = gS[(r * H + h) * 9 + k] * inv_sqrt_d;
+                        const double kw = K[((size_t)pod * H + h) * 9 + k];
+                        for (int c = 0; c < D; ++c) {
+                            const size_t iq = q * C + h * D + c, ir = r * C + h * D + c;
+                            gV[iq] += a * gVt[ir];
+                            gI[iq] += gs * P[ir];
+                            gx[iq] += kw * gU[ir];
+                        }
+                    }
+                }
+            }
+    }
+    // S1 backward
+    for (size_t i = 0; i < n; ++i) {
+        gP[i] = pt[i] > 0.0 ? gP[i] : 0.0;
+        gI[i] *= gelu_tanh_grad(it[i]);
+    }
+    project_back_input(d, gP.data(), WP, gx.data());
+    project_back_input(d, gI.data(), WI, gx.data());
+    project_back_input(d, gV.data(), WV, gx.data());
+    to_f(gx, gX);
+    if (gWP) project_back_weight(d, x.data(), gP.data(), gWP);
+    if (gWI) project_back_weight(d, x.data(), gI.data(), gWI);
+    if (gWV) project_back_weight(d, x.data(), gV.data(), gWV);
+    if (gK) to_f(gKd, gK);
+    if (gmu) to_f(gmud, gmu);
+    if (gsigma) to_f(gsgd, gsigma);
+    if (gM) to_f(gMd, gM);
     return 0;
 }
 

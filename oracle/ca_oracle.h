@@ -49,6 +49,15 @@ int oracle_step(const oracle_ca_cfg* cfg, const float* X_in, const float* WP, co
                 const float* WV, const float* K, const float* mu, const float* sigma,
                 const float* M, float* X_out, int n_steps, double* mass_in, double* mass_out);
 
+/* One step (parallel projections) and the loss L = mean (X_out - T)^2; with gX
+ * non-NULL also dL/dX and, for each non-NULL pointer, the parameter gradients
+ * (shapes as the parameters). Returns -1 for chained projections. */
+int oracle_step_backward(const oracle_ca_cfg* cfg, const float* X, const float* WP,
+                         const float* WI, const float* WV, const float* K, const float* mu,
+                         const float* sigma, const float* M, const float* T, double* loss,
+                         float* gX, float* gWP, float* gWI, float* gWV, float* gK, float* gmu,
+                         float* gsigma, float* gM);
+
 int oracle_gram(const oracle_ca_cfg* cfg, const float* X, double* A);
 int oracle_jacobi_eigs(const double* A, int n, double* eig_desc, int max_sweeps, double tol);
 double oracle_effective_rank(const double* sv, int n);

@@ -25,7 +25,7 @@ EXPORTS = (
     "slime_ca_flow_lenia", "slime_ca_step", "slime_ca_mass", "slime_ca_fitness",
     "slime_ca_fitness_sweeps", "slime_ca_init_from_field", "slime_ca_field_from_state",
     "slime_ca_uses_mfma", "slime_ca_set_timing", "slime_ca_timings", "slime_ca_last_error",
-    "slime_neural_ca_update",
+    "slime_neural_ca_update", "slime_ca_backward",
 )
 
 
@@ -44,6 +44,11 @@ class MultiHeadCAState(ctypes.Structure):
     """slime_multihead_ca_state: the per-generation buffers of MultiHeadCAState."""
     _fields_ = [("mass_buffer", ctypes.c_void_p), ("ca_input", ctypes.c_void_p),
                 ("ca_output", ctypes.c_void_p)]
+
+
+class Grads(ctypes.Structure):
+    """slime_ca_grads: device fp32 parameter-gradient pointers (NULL allowed)."""
+    _fields_ = [(n, ctypes.c_void_p) for n in ("WP", "WI", "WV", "K", "mu", "sigma", "M")]
 
 
 class SlimeError(RuntimeError):
@@ -81,6 +86,8 @@ def load() -> ctypes.CDLL:
         "slime_ca_timings": [vp, vp, vp, vp, vp],
         "slime_ca_last_error": [],
         "slime_neural_ca_update": [vp, ctypes.POINTER(MultiHeadCAState), vp, vp, i, vp],
+        "slime_ca_backward": [vp, vp, vp, vp, ctypes.POINTER(Grads), ctypes.POINTER(ctypes.c_double),
+                              vp],
     }
     for name, args in sig.items():
         fn = getattr(lib, name)

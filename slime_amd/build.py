@@ -19,7 +19,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libslime_ca.so")
-SOURCES = ["api.cpp", "gemm.hip", "stencil.hip", "mass.hip", "fitness.hip", "organism.hip"]
+SOURCES = ["api.cpp", "gemm.hip", "stencil.hip", "mass.hip", "fitness.hip", "organism.hip",
+           "backward.hip"]
 ARCH = "gfx950"
 
 

@@ -152,6 +152,33 @@ class Pseudopod:
                                           mo.ctypes.data_as(ctypes.c_void_p)))
         return mi, mo
 
+    # -- gradient (update_gradients, declared only: slime/proto/model.cu:7,13) ----------
+    def backward(self, x, target, params: bool = True, stream=None):
+        """One step from ``x`` and the gradient of L = mean((step(x) - target)^2).
+
+        Returns ``(loss, grad_x, grads)``: the loss as a float, dL/dx as a float32
+        CUDA tensor of the state's shape and, when ``params``, a dict of float32
+        CUDA tensors WP, WI, WV, K, mu, sigma, M shaped as the parameters (else
+        an empty dict). Parallel projections only."""
+        torch = _torch()
+        self._check_state(x, "x")
+        self._check_state(target, "target")
+        gx = torch.empty(self.state_shape, dtype=torch.float32, device="cuda")
+        grads = {}
+        if params:
+            C, H, pods = self.C, self.H, self.pods
+            g = (pods, self.G, self.G, H) if self.growth_per_cell else (pods, H)
+            shapes = {"WP": (pods, C, C), "WI": (pods, C, C), "WV": (pods, C, C),
+                      "K": (pods, H, 9), "mu": g, "sigma": g, "M": (pods, H, H)}
+            grads = {k: torch.empty(v, dtype=torch.float32, device="cuda") for k, v in shapes.items()}
+        gs = _lib.Grads(*[grads[k].data_ptr() if k in grads else None
+                          for k in ("WP", "WI", "WV", "K", "mu", "sigma", "M")])
+        loss = ctypes.c_double()
+        _lib.check(self.lib.slime_ca_backward(self._h, _ptr(x), _ptr(target), _ptr(gx),
+                                              ctypes.byref(gs), ctypes.byref(loss),
+                                              _stream(stream)))
+        return loss.value, gx, grads
+
     # -- fitness (slime/kernels/warp_ca.cu:178-226) -------------------------------------
     def fitness(self, hist, stream=None):
         """``hist``: [T, B, G, G, C] CUDA tensor -> (erank, coherence, fitness), [B, H] each."""

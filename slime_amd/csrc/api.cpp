@@ -56,6 +56,25 @@ struct slime_ca {
     int* sweeps = nullptr;     // [B*H]
     float* org_fit = nullptr;  // [3][B*H] erank, coherence, fitness of slime_neural_ca_update
 
+    // slime_ca_backward (allocated on its first call)
+    void* Wcat = nullptr;      // [pods][C][3C] = [W_P | W_I | W_V] row k (input channel), dtype
+    std::vector<float> wcat_host;
+    void* Ipre = nullptr;      // I before the GELU, dtype
+    double* bw_lpart = nullptr;
+    float* bw_coef = nullptr;
+    double* bw_loss = nullptr;
+    float* bw_gU = nullptr;
+    float* bw_gVt = nullptr;
+    float* bw_att = nullptr;
+    float* bw_gS = nullptr;
+    void* bw_G3 = nullptr;
+    float* bw_gXd = nullptr;
+    float* bw_ppart = nullptr;
+    float* bw_gcell = nullptr;
+    void* bw_gXp = nullptr;
+    float* bw_dwpart = nullptr;
+    float* bw_y32 = nullptr;   // fp32 unscaled output of the taped step (fp32 state only)
+
     // Optional per-kernel timing: event pairs recorded around launches.
     bool timing = false;
     std::vector<hipEvent_t> ev_pool;
@@ -154,7 +173,10 @@ void release(slime_ca* h) {
     h->ev_pool.clear();
     void* ptrs[] = {h->Wtm, h->Wt, h->K, h->mu, h->sigma, h->M, h->kmat, h->P, h->I, h->V, h->S[0], h->S[1], h->Sf,
                     h->part_in, h->part_out, h->scale[0], h->scale[1], h->unit_scale,
-                    h->mass_in, h->mass_out, h->gram_part, h->mom_part, h->sweeps, h->org_fit};
+                    h->mass_in, h->mass_out, h->gram_part, h->mom_part, h->sweeps, h->org_fit,
+                    h->Wcat, h->Ipre, h->bw_lpart, h->bw_coef, h->bw_loss, h->bw_gU, h->bw_gVt,
+                    h->bw_att, h->bw_gS, h->bw_G3, h->bw_gXd, h->bw_ppart, h->bw_gcell, h->bw_gXp,
+                    h->bw_dwpart, h->bw_y32};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
 }
@@ -399,6 +421,19 @@ int slime_ca_set_params(slime_ca* h, const slime_ca_params* p) {
                               hipMemcpyHostToDevice));
         }
     }
+    // [W_P | W_I | W_V] by input channel, for the backward's dX GEMM (uploaded by
+    // slime_ca_backward when first needed).
+    h->wcat_host.assign((size_t)c.pods * C * 3 * C, 0.f);
+    for (int q = 0; q < c.pods; ++q) {
+        const float* src[3] = {p->WP + (size_t)q * CC, p->WI + (size_t)q * CC, p->WV + (size_t)q * CC};
+        for (int pl = 0; pl < 3; ++pl)
+            for (size_t k = 0; k < C; ++k)
+                std::memcpy(&h->wcat_host[((size_t)q * C + k) * 3 * C + pl * C], src[pl] + k * C, C * 4);
+    }
+    if (h->Wcat) {
+        (void)hipFree(h->Wcat);
+        h->Wcat = nullptr;
+    }
     const size_t ng = n_param_growth(c);
     for (size_t i = 0; i < ng; ++i)
         if (!std::isfinite(p->sigma[i]) || !std::isfinite(p->mu[i]))
@@ -567,6 +602,163 @@ int slime_neural_ca_update(slime_ca* h, const slime_multihead_ca_state* st, floa
     if (rc) return rc;
     HIP_TRY(launch_organism_report(h->mass_out, h->org_fit, h->cfg.H, st->mass_buffer,
                                    erank_hist + generation, s));
+    return SLIME_OK;
+}
+
+int slime_ca_backward(slime_ca* h, const void* x_in, const void* target, float* grad_x,
+                      const slime_ca_grads* grads, double* loss, void* stream) {
+    int rc = use_handle(h);
+    if (rc) return rc;
+    if (!h->params_set) return fail(SLIME_ESTATE, "slime_ca_set_params has not been called");
+    if (!x_in || !target || !grad_x) return fail(SLIME_EINVAL, "a tensor pointer is NULL");
+    const slime_ca_config& c = h->cfg;
+    if (c.pvi_chain) return fail(SLIME_EINVAL, "the backward supports parallel projections only");
+    const size_t C = h->C, BH = (size_t)c.B * c.H, n = (size_t)h->state_elems;
+    const size_t cells = (size_t)c.B * c.G * c.G;
+    const int lchunks = backward_loss_chunks(c.G);
+    const int nW = 128;
+    const long long rows_pod = (long long)(c.B / c.pods) * c.G * c.G;
+    const int dw_chunks = backward_dw_chunks_per_pod(rows_pod);
+    const bool want_w = grads && (grads->WP || grads->WI || grads->WV);
+    // work buffers, allocated on first use
+    if (!h->Wcat) {
+        rc = dalloc(&h->Wcat, h->wcat_host.size() * h->elem);
+        if (rc) return rc;
+        if (h->elem == 2) {
+            std::vector<uint16_t> wb(h->wcat_host.size());
+            for (size_t i = 0; i < wb.size(); ++i) {
+                uint32_t u;
+                std::memcpy(&u, &h->wcat_host[i], 4);
+                u += 0x7FFFu + ((u >> 16) & 1u);  // round to nearest even, as the device cvt
+                wb[i] = (uint16_t)(u >> 16);
+            }
+            HIP_TRY(hipMemcpy(h->Wcat, wb.data(), wb.size() * 2, hipMemcpyHostToDevice));
+        } else {
+            HIP_TRY(hipMemcpy(h->Wcat, h->wcat_host.data(), h->wcat_host.size() * 4, hipMemcpyHostToDevice));
+        }
+    }
+    rc = 0;
+    if (!h->Ipre) rc = rc ? rc : dalloc(&h->Ipre, n * h->elem);
+    if (!h->bw_lpart) rc = rc ? rc : dalloc_t(&h->bw_lpart, BH * lchunks * 3 * 8);
+    if (!h->bw_coef) rc = rc ? rc : dalloc_t(&h->bw_coef, BH * 2 * 4);
+    if (!h->bw_loss) rc = rc ? rc : dalloc_t(&h->bw_loss, BH * 8);
+    if (!h->bw_gU) rc = rc ? rc : dalloc_t(&h->bw_gU, n * 4);
+    if (!h->bw_gVt) rc = rc ? rc : dalloc_t(&h->bw_gVt, n * 4);
+    if (!h->bw_att) rc = rc ? rc : dalloc_t(&h->bw_att, cells * c.H * 9 * 4);
+    if (!h->bw_gS) rc = rc ? rc : dalloc_t(&h->bw_gS, cells * c.H * 9 * 4);
+    if (!h->bw_G3) rc = rc ? rc : dalloc(&h->bw_G3, n * 3 * h->elem);
+    if (!h->bw_gXd) rc = rc ? rc : dalloc_t(&h->bw_gXd, n * 4);
+    if (!h->bw_ppart)
+        rc = rc ? rc : dalloc_t(&h->bw_ppart, (size_t)c.pods * c.H * nW * backward_part_floats() * 4);
+    if (c.growth_per_cell && !h->bw_gcell) rc = rc ? rc : dalloc_t(&h->bw_gcell, cells * c.H * 2 * 4);
+    if (!h->bw_gXp) rc = rc ? rc : dalloc(&h->bw_gXp, n * h->elem);
+    if (want_w && !h->bw_dwpart)
+        rc = rc ? rc : dalloc_t(&h->bw_dwpart, (size_t)c.pods * dw_chunks * C * 3 * C * 4);
+    if (!h->Sf && !h->bw_y32) rc = rc ? rc : dalloc_t(&h->bw_y32, n * 4);
+    if (rc) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    h->last_stream = s;
+
+    // forward tape: P, I, V; I before its GELU; the unscaled fp32 output and the scale
+    rc = run_project(h, x_in, nullptr, h->P, h->I, h->V, s);
+    if (rc) return rc;
+    {
+        GemmArgs g{};
+        g.A = x_in;
+        g.Bt = static_cast<const char*>(h->Wt) + C * C * h->elem;  // plane I of the per-batch weights
+        g.bt_batch_stride = 3LL * C * C;
+        g.rows_per_batch = c.G * c.G;
+        g.M = c.B * c.G * c.G;
+        g.N = (int)C;
+        g.K = (int)C;
+        g.out[0] = h->Ipre;
+        g.ncol = (int)C;
+        g.act[0] = 0;
+        HIP_TRY(launch_gemm(c.dtype, g, s));
+    }
+    float* y32 = h->Sf ? h->Sf : h->bw_y32;
+    float* rs = h->scale[0];
+    rc = run_stencil(h, x_in, nullptr, h->P, h->I, h->V, y32, 1, rs, s);
+    if (rc) return rc;
+
+    // backward through S7..S2 and the activations
+    BackwardArgs a{};
+    a.X = x_in;
+    a.P = h->P;
+    a.I = h->I;
+    a.V = h->V;
+    a.Ipre = h->Ipre;
+    a.Y = y32;
+    a.T = target;
+    a.scale = rs;
+    a.K = h->K;
+    a.mu = h->mu;
+    a.sigma = h->sigma;
+    a.M = h->M;
+    a.B = c.B;
+    a.G = c.G;
+    a.D = c.D;
+    a.per_pod = c.B / c.pods;
+    a.pods = c.pods;
+    a.per_cell = c.growth_per_cell;
+    a.dt = c.dt;
+    a.inv_n = (float)(1.0 / (double)n);
+    a.lpart = h->bw_lpart;
+    a.lchunks = lchunks;
+    a.coef = h->bw_coef;
+    a.loss_bh = h->bw_loss;
+    a.gU = h->bw_gU;
+    a.gVt = h->bw_gVt;
+    a.att = h->bw_att;
+    a.gS = h->bw_gS;
+    a.G3 = h->bw_G3;
+    a.gXd = h->bw_gXd;
+    a.ppart = h->bw_ppart;
+    a.nW = nW;
+    a.gcell = h->bw_gcell;
+    if (grads) {
+        a.gK = grads->K;
+        a.gmu = grads->mu;
+        a.gsigma = grads->sigma;
+        a.gM = grads->M;
+    }
+    HIP_TRY(launch_backward_stencil(c.dtype, a, s));
+    // gX += [gP~ | gI~ | gV] [W_P | W_I | W_V]^T
+    {
+        GemmArgs g{};
+        g.A = h->bw_G3;
+        g.Bt = h->Wcat;
+        g.bt_batch_stride = 3LL * C * C;
+        g.rows_per_batch = (int)rows_pod;
+        g.M = c.B * c.G * c.G;
+        g.N = (int)C;
+        g.K = (int)(3 * C);
+        g.out[0] = h->bw_gXp;
+        g.ncol = (int)C;
+        g.act[0] = 0;
+        HIP_TRY(launch_gemm(c.dtype, g, s));
+    }
+    HIP_TRY(launch_backward_final(c.dtype, h->bw_gXd, h->bw_gXp, grad_x, (long long)n, s));
+    if (want_w) {
+        DwArgs d{};
+        d.part = h->bw_dwpart;
+        d.C = (int)C;
+        d.pods = c.pods;
+        d.chunks_per_pod = dw_chunks;
+        d.rows_per_pod = rows_pod;
+        d.gWP = grads->WP;
+        d.gWI = grads->WI;
+        d.gWV = grads->WV;
+        HIP_TRY(launch_backward_dw(c.dtype, a, d, s));
+    }
+    if (loss) {
+        std::vector<double> l(BH);
+        HIP_TRY(hipStreamSynchronize(s));
+        HIP_TRY(hipMemcpy(l.data(), h->bw_loss, BH * 8, hipMemcpyDeviceToHost));
+        double tot = 0.0;
+        for (double v : l) tot += v;
+        *loss = tot / (double)n;
+    }
     return SLIME_OK;
 }
 

@@ -1,0 +1,468 @@
+// backward.hip — gradient of one CA step under the MSE loss (configuration c5):
+// L = mean over all elements of (Y' - T)^2, Y' the conserved output of one step
+// with parallel P/I/V projections.
+//
+// The reference declares gradients (gradients_d, update_gradients,
+// slime/proto/model.cu:7,13) but never computes any; the chain rule here follows
+// the forward stages S1-S7 (slime/core/pseudopod.cu:41-253 and the sources listed
+// in stencil.hip), stage by stage in reverse:
+//   S7  gY' = 2 (Y' - T)/N;  Q_o = sum gY' Y_o;  gY_o = r_o (gY' - Q_o/B_o) and
+//       gX_o += Q_o/B_o when |B_o| > 1e-6 (B_o = sum Y_o, r_o = A_o/B_o), else gY_o = gY'
+//   S6  gZ_h = sum_o M[o][h] gY_o;  gM[o][h] += sum gY_o Z_h;  gX += gZ;
+//       gg = dt gZ Vt;  gVt = dt gZ g
+//   S3  gU = gg (-4 t e^{-t^2}) / (sigma + 1e-7);  gmu += -gU;  gsigma += -gU t
+//   S2  gX(n_k(r)) += K[h][k] gU(r);  gK[h][k] += sum gU(r) X(n_k(r))
+//   S5  gV(n_k(r)) += a_k gVt(r);  ga_k = <gVt(r), V(n_k(r))>
+//   S4  gs_k = a_k (ga_k - sum_j a_j ga_j);  gP(r) += sum_k gs_k I(n_k) / sqrt(D);
+//       gI(n_k(r)) += gs_k P(r) / sqrt(D)
+//   S1  gP~ = gP [P > 0];  gI~ = gI GELU'(I~);  gX += [gP~|gI~|gV] [W_P|W_I|W_V]^T
+//       (MFMA GEMM, gemm.hip);  gW_p = X^T gp (per pod)
+// Scatters run as gathers: cell q collects from the cells r = q - offset_k whose
+// neighbour k it is, so no atomics are needed and every sum has a fixed order.
+//
+// Work split: one lane per (cell, head, channel) with the D lanes of a (cell,
+// head) adjacent; the per-(cell, head) dot products reduce over those D lanes.
+// Parameter partial sums are kept per workgroup, each workgroup owning one
+// (pod, head), and added in a fixed order by the finalize kernels.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace slime {
+namespace {
+
+__device__ __forceinline__ int wrapb(int v, int G) { return v < 0 ? v + G : (v >= G ? v - G : v); }
+
+template <typename T>
+__device__ __forceinline__ float ld(const void* p, long long i) {
+    return Store<T>::to_f32(static_cast<const T*>(p)[i]);
+}
+
+// Sum over groups of kD adjacent lanes (kD = 8 .. 64), every lane of the group
+// receiving the sum.
+template <int kD>
+__device__ __forceinline__ float dsum(float v) {
+#pragma unroll
+    for (int m = kD / 2; m > 0; m >>= 1) v += __shfl_xor(v, m, 64);
+    return v;
+}
+
+__device__ __forceinline__ float gelu_grad(float x) {
+    const float c0 = 0.7978845608028654f, c1 = 0.044715f;
+    const float th = tanhf(c0 * (x + c1 * x * x * x));
+    return 0.5f * (1.0f + th) + 0.5f * x * (1.0f - th * th) * c0 * (1.0f + 3.0f * c1 * x * x);
+}
+
+// ---- S7: loss, Q_o, B_o partial sums ---------------------------------------------------
+// Block (b, chunk) covers kLossCells cells of batch b; thread t owns channels t,
+// t + 256, ... and accumulates per head in fp64.
+constexpr int kLossCells = 64;
+
+template <typename T>
+__global__ __launch_bounds__(256) void bw_loss_partial_kernel(BackwardArgs a) {
+    const int b = blockIdx.y, chunk = blockIdx.x;
+    const int C = kHeads * a.D;
+    const long long cells = (long long)a.G * a.G;
+    const double N = (double)a.B * (double)cells * C;
+    __shared__ double s[3][kHeads][256];
+    double acc[3][kHeads];
+#pragma unroll
+    for (int q = 0; q < 3; ++q)
+#pragma unroll
+        for (int h = 0; h < kHeads; ++h) acc[q][h] = 0.0;
+    for (int c0 = 0; c0 < kLossCells; ++c0) {
+        const long long cell = (long long)chunk * kLossCells + c0;
+        if (cell >= cells) break;
+        const long long base = ((long long)b * cells + cell) * C;
+        for (int ch = threadIdx.x; ch < C; ch += 256) {
+            const int h = ch / a.D;
+            const float r = a.scale[b * kHeads + h];
+            const double y = a.Y[base + ch];
+            const double e = (double)r * y - (double)ld<T>(a.T, base + ch);
+#pragma unroll
+            for (int hh = 0; hh < kHeads; ++hh)
+                if (hh == h) {
+                    acc[0][hh] += e * e;
+                    acc[1][hh] += 2.0 * e / N * y;
+                    acc[2][hh] += y;
+                }
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < 3; ++q)
+#pragma unroll
+        for (int h = 0; h < kHeads; ++h) s[q][h][threadIdx.x] = acc[q][h];
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w)
+#pragma unroll
+            for (int q = 0; q < 3; ++q)
+#pragma unroll
+                for (int h = 0; h < kHeads; ++h) s[q][h][threadIdx.x] += s[q][h][threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x < 3 * kHeads) {
+        const int q = threadIdx.x / kHeads, h = threadIdx.x % kHeads;
+        a.lpart[(((long long)b * kHeads + h) * a.lchunks + chunk) * 3 + q] = s[q][h][0];
+    }
+}
+
+// One thread per (b, head): fixed-order sums of the partials, then the S7 chain
+// coefficients: gY = cY (gY' - cQ), and cQ is also the uniform direct term of gX.
+__global__ __launch_bounds__(64) void bw_loss_finalize_kernel(BackwardArgs a) {
+    const int bh = blockIdx.x * 64 + threadIdx.x;
+    if (bh >= a.B * kHeads) return;
+    double l = 0.0, q = 0.0, bs = 0.0;
+    for (int c = 0; c < a.lchunks; ++c) {
+        const double* p = a.lpart + ((long long)bh * a.lchunks + c) * 3;
+        l += p[0];
+        q += p[1];
+        bs += p[2];
+    }
+    const bool guard = fabs(bs) > 1e-6;
+    a.coef[bh * 2 + 0] = guard ? a.scale[bh] : 1.0f;
+    a.coef[bh * 2 + 1] = guard ? (float)(q / bs) : 0.0f;
+    a.loss_bh[bh] = l;
+}
+
+// ---- per (cell, head): S7, S6, S3, S5, S4 backward and the tape for the gathers ------------
+// Block (pod, head, w): the lanes of group g handle cells i = w*gpw + g (+ stride)
+// of the pod's batches for that head. Per-thread parameter partials (M column h,
+// K row h, mu, sigma) are reduced over the block and written once.
+constexpr int kPartF = kHeads + 9 + 2;  // gM[o][h] (8), gK[h][k] (9), gmu, gsigma
+
+template <typename T, int kD>
+__global__ __launch_bounds__(256) void bw_cell_kernel(BackwardArgs a) {
+    constexpr int H = kHeads, C = H * kD, kGroups = 256 / kD;
+    const int G = a.G;
+    const long long cells = (long long)G * G;
+    const int w = blockIdx.x % a.nW;
+    const int h = (blockIdx.x / a.nW) % H;
+    const int pod = blockIdx.x / (a.nW * H);
+    const int grp = threadIdx.x / kD, c = threadIdx.x % kD;
+    const long long pod_cells = (long long)a.per_pod * cells;
+    const float inv_sqrt_d = 1.0f / __builtin_sqrtf((float)kD);
+    const float dt = a.dt;
+    float mcol[H];
+#pragma unroll
+    for (int o = 0; o < H; ++o) mcol[o] = a.M[(pod * H + o) * H + h];
+    float kw[9];
+#pragma unroll
+    for (int k = 0; k < 9; ++k) kw[k] = a.K[(pod * H + h) * 9 + k];
+    float pM[H], pK[9], pmu = 0.f, psg = 0.f;
+#pragma unroll
+    for (int o = 0; o < H; ++o) pM[o] = 0.f;
+#pragma unroll
+    for (int k = 0; k < 9; ++k) pK[k] = 0.f;
+
+    for (long long i = (long long)w * kGroups + grp; i < pod_cells; i += (long long)a.nW * kGroups) {
+        const int b = pod * a.per_pod + (int)(i / cells);
+        const long long cell = i % cells;
+        const int y = (int)(cell / G), x = (int)(cell % G);
+        const long long r = (long long)b * cells + cell;
+        const long long ir = r * C + h * kD + c;
+        // S7 -> gY for every output head o at (r, c); S6 -> gZ_h
+        float gz = 0.f;
+        float gy[H];
+#pragma unroll
+        for (int o = 0; o < H; ++o) {
+            const long long io = r * C + o * kD + c;
+            const float rs = a.scale[b * H + o];
+            const float e = rs * a.Y[io] - ld<T>(a.T, io);
+            const float gyp = 2.0f * e * a.inv_n;
+            gy[o] = a.coef[(b * H + o) * 2] * (gyp - a.coef[(b * H + o) * 2 + 1]);
+            gz = __builtin_fmaf(mcol[o], gy[o], gz);
+        }
+        // forward locals of head h at r
+        long long nb[9];
+        float u = 0.f;
+#pragma unroll
+        for (int k = 0; k < 9; ++k) {
+            const long long q = (long long)b * cells + (long long)wrapb(y + k / 3 - 1, G) * G +
+                                wrapb(x + k % 3 - 1, G);
+            nb[k] = q * C + h * kD + c;
+            u = __builtin_fmaf(kw[k], ld<T>(a.X, nb[k]), u);
+        }
+        float mu, sg;
+        if (a.per_cell) {
+            const long long pi = ((long long)pod * cells + cell) * H + h;
+            mu = a.mu[pi];
+            sg = a.sigma[pi];
+        } else {
+            mu = a.mu[pod * H + h];
+            sg = a.sigma[pod * H + h];
+        }
+        const float sp = sg + 1e-7f;
+        const float t = (u - mu) / sp;
+        const float et = __expf(-t * t);
+        const float g = 2.0f * et - 1.0f;
+        const float pc = ld<T>(a.P, ir);
+        float s[9], mx = -3.0e38f;
+#pragma unroll
+        for (int k = 0; k < 9; ++k) {
+            s[k] = dsum<kD>(pc * ld<T>(a.I, nb[k])) * inv_sqrt_d;
+            mx = fmaxf(mx, s[k]);
+        }
+        float den = 0.f;
+#pragma unroll
+        for (int k = 0; k < 9; ++k) {
+            s[k] = __expf(s[k] - mx);
+            den += s[k];
+        }
+        float vt = 0.f, vn[9];
+#pragma unroll
+        for (int k = 0; k < 9; ++k) {
+            s[k] /= den;  // a_k
+            vn[k] = ld<T>(a.V, nb[k]);
+            vt = __builtin_fmaf(s[k], vn[k], vt);
+        }
+        const float xr = ld<T>(a.X, ir);
+        const float z = __builtin_fmaf(dt * g, vt, xr);
+#pragma unroll
+        for (int o = 0; o < H; ++o) pM[o] = __builtin_fmaf(gy[o], z, pM[o]);
+        // S6, S3
+        const float gg = dt * gz * vt, gvt = dt * gz * g;
+        const float gu = gg * (-4.0f * t * et) / sp;
+        if (a.per_cell) {
+            const float smu = dsum<kD>(-gu), ssg = dsum<kD>(-gu * t);
+            if (c == 0) {
+                a.gcell[(r * H + h) * 2 + 0] = smu;
+                a.gcell[(r * H + h) * 2 + 1] = ssg;
+            }
+        } else {
+            pmu -= gu;
+            psg -= gu * t;
+        }
+#pragma unroll
+        for (int k = 0; k < 9; ++k) pK[k] = __builtin_fmaf(gu, ld<T>(a.X, nb[k]), pK[k]);
+        // S5, S4
+        float ga[9], sa = 0.f;
+#pragma unroll
+        for (int k = 0; k < 9; ++k) {
+            ga[k] = dsum<kD>(gvt * vn[k]);
+            sa = __builtin_fmaf(s[k], ga[k], sa);
+        }
+        float gp = 0.f;
+#pragma unroll
+        for (int k = 0; k < 9; ++k) {
+            const float gs = s[k] * (ga[k] - sa);
+            gp = __builtin_fmaf(gs * inv_sqrt_d, ld<T>(a.I, nb[k]), gp);
+            if (k % kD == c) {  // the tape for the gathers: a_k and gs_k per (r, h)
+                a.att[(r * H + h) * 9 + k] = s[k];
+                a.gS[(r * H + h) * 9 + k] = gs;
+            }
+        }
+        a.gU[ir] = gu;
+        a.gVt[ir] = gvt;
+        // gP~ -> plane 0 of G3; the direct part of gX
+        const float gpt = pc > 0.f ? gp : 0.f;
+        static_cast<T*>(a.G3)[r * 3 * C + h * kD + c] = Store<T>::from_f32(gpt);
+        a.gXd[ir] = gz + a.coef[(b * H + h) * 2 + 1];
+    }
+    // block reduction of the parameter partials, fixed order
+    __shared__ float red[kPartF][256];
+#pragma unroll
+    for (int o = 0; o < H; ++o) red[o][threadIdx.x] = pM[o];
+#pragma unroll
+    for (int k = 0; k < 9; ++k) red[H + k][threadIdx.x] = pK[k];
+    red[H + 9][threadIdx.x] = pmu;
+    red[H + 10][threadIdx.x] = psg;
+    __syncthreads();
+    for (int s2 = 128; s2 > 0; s2 >>= 1) {
+        if ((int)threadIdx.x < s2)
+            for (int q = 0; q < kPartF; ++q) red[q][threadIdx.x] += red[q][threadIdx.x + s2];
+        __syncthreads();
+    }
+    if ((int)threadIdx.x < kPartF)
+        a.ppart[(long long)blockIdx.x * kPartF + threadIdx.x] = red[threadIdx.x][0];
+}
+
+// ---- gathers: gV, gI~ (planes 2 and 1 of G3) and the potential's transpose -------------------
+template <typename T, int kD>
+__global__ __launch_bounds__(256) void bw_gather_kernel(BackwardArgs a) {
+    constexpr int H = kHeads, C = H * kD;
+    const int G = a.G;
+    const long long cells = (long long)G * G;
+    const long long e = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (e >= (long long)a.B * cells * C) return;
+    const long long q = e / C;
+    const int ch = (int)(e % C), h = ch / kD;
+    const int b = (int)(q / cells);
+    const long long cell = q % cells;
+    const int y = (int)(cell / G), x = (int)(cell % G);
+    const int pod = b / a.per_pod;
+    const float inv_sqrt_d = 1.0f / __builtin_sqrtf((float)kD);
+    float gv = 0.f, gi = 0.f, gx = 0.f;
+#pragma unroll
+    for (int k = 0; k < 9; ++k) {
+        // r = q - offset_k: the cell whose neighbour k is q
+        const long long r = (long long)b * cells + (long long)wrapb(y - (k / 3 - 1), G) * G +
+                            wrapb(x - (k % 3 - 1), G);
+        const long long ir = r * C + ch;
+        const float ak = a.att[(r * H + h) * 9 + k], gs = a.gS[(r * H + h) * 9 + k];
+        gv = __builtin_fmaf(ak, a.gVt[ir], gv);
+        gi = __builtin_fmaf(gs * inv_sqrt_d, ld<T>(a.P, ir), gi);
+        gx = __builtin_fmaf(a.K[(pod * H + h) * 9 + k], a.gU[ir], gx);
+    }
+    T* g3 = static_cast<T*>(a.G3) + q * 3 * C;
+    g3[C + ch] = Store<T>::from_f32(gi * gelu_grad(ld<T>(a.Ipre, e)));
+    g3[2 * C + ch] = Store<T>::from_f32(gv);
+    a.gXd[e] += gx;
+}
+
+// ---- parameter finalize: fixed-order sums of the per-block partials ----------------------------
+__global__ __launch_bounds__(64) void bw_param_finalize_kernel(BackwardArgs a) {
+    // one thread per (pod, head, quantity)
+    const int idx = blockIdx.x * 64 + threadIdx.x;
+    if (idx >= a.pods * kHeads * kPartF) return;
+    const int q = idx % kPartF, h = (idx / kPartF) % kHeads, pod = idx / (kPartF * kHeads);
+    float sum = 0.f;
+    for (int w = 0; w < a.nW; ++w)
+        sum += a.ppart[((long long)(pod * kHeads + h) * a.nW + w) * kPartF + q];
+    if (q < kHeads) {
+        if (a.gM) a.gM[(pod * kHeads + q) * kHeads + h] = sum;  // gM[o = q][h]
+    } else if (q < kHeads + 9) {
+        if (a.gK) a.gK[(pod * kHeads + h) * 9 + (q - kHeads)] = sum;
+    } else if (!a.per_cell) {
+        float* dst = q == kHeads + 9 ? a.gmu : a.gsigma;
+        if (dst) dst[pod * kHeads + h] = sum;
+    }
+}
+
+// per-cell growth parameters: sum over the pod's batches
+__global__ __launch_bounds__(256) void bw_cell_param_finalize_kernel(BackwardArgs a) {
+    const long long cells = (long long)a.G * a.G;
+    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;  // (pod, cell, h)
+    if (idx >= (long long)a.pods * cells * kHeads) return;
+    const int pod = (int)(idx / (cells * kHeads));
+    const long long ch = idx % (cells * kHeads);
+    float smu = 0.f, ssg = 0.f;
+    for (int j = 0; j < a.per_pod; ++j) {
+        const long long r = (long long)(pod * a.per_pod + j) * cells * kHeads + ch;
+        smu += a.gcell[r * 2 + 0];
+        ssg += a.gcell[r * 2 + 1];
+    }
+    if (a.gmu) a.gmu[idx] = smu;
+    if (a.gsigma) a.gsigma[idx] = ssg;
+}
+
+// ---- weight gradients gW_p[pod][k][j] = sum over the pod's rows of X[r][k] G_p[r][j] ----------
+// Block (k tile, j tile, chunk): a 64 x 64 output tile over kWRows rows, 4 x 4
+// per thread, operands staged through LDS 16 rows at a time; chunks are added in
+// order by bw_dw_reduce_kernel.
+constexpr int kWRows = 4096;
+
+template <typename T>
+__global__ __launch_bounds__(256) void bw_dw_partial_kernel(BackwardArgs a, DwArgs d) {
+    const int C = d.C, N3 = 3 * C;
+    const int kt = blockIdx.x, jt = blockIdx.y, chunk = blockIdx.z;
+    const long long rows = d.rows_per_pod;
+    const int pod = chunk / d.chunks_per_pod;
+    const long long r0 = (long long)pod * rows + (long long)(chunk % d.chunks_per_pod) * kWRows;
+    const long long r1 = min(r0 + kWRows, (long long)(pod + 1) * rows);
+    __shared__ float sx[16][64], sg[16][64];
+    const int tk = (threadIdx.x / 16) * 4, tj = (threadIdx.x % 16) * 4;
+    float acc[4][4] = {};
+    for (long long rb = r0; rb < r1; rb += 16) {
+        for (int e = threadIdx.x; e < 16 * 64; e += 256) {
+            const int rr = e / 64, cc = e % 64;
+            const long long r = rb + rr;
+            sx[rr][cc] = r < r1 ? ld<T>(a.X, r * C + kt * 64 + cc) : 0.f;
+            sg[rr][cc] = r < r1 ? ld<T>(a.G3, r * N3 + jt * 64 + cc) : 0.f;
+        }
+        __syncthreads();
+#pragma unroll 4
+        for (int rr = 0; rr < 16; ++rr)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_fmaf(sx[rr][tk + i], sg[rr][tj + j], acc[i][j]);
+        __syncthreads();
+    }
+    float* out = d.part + (long long)chunk * C * N3;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) out[(long long)(kt * 64 + tk + i) * N3 + jt * 64 + tj + j] = acc[i][j];
+}
+
+__global__ __launch_bounds__(256) void bw_dw_reduce_kernel(DwArgs d) {
+    const int C = d.C, N3 = 3 * C;
+    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;  // (pod, k, j)
+    if (idx >= (long long)d.pods * C * N3) return;
+    const int pod = (int)(idx / ((long long)C * N3));
+    const long long kj = idx % ((long long)C * N3);
+    float sum = 0.f;
+    for (int c = 0; c < d.chunks_per_pod; ++c)
+        sum += d.part[((long long)(pod * d.chunks_per_pod + c)) * C * N3 + kj];
+    const int k = (int)(kj / N3), j = (int)(kj % N3), p = j / C;
+    float* dst = p == 0 ? d.gWP : p == 1 ? d.gWI : d.gWV;
+    if (dst) dst[((long long)pod * C + k) * C + (j - p * C)] = sum;
+}
+
+// grad_x = direct part + the projections' part (GEMM output, storage type)
+template <typename T>
+__global__ __launch_bounds__(256) void bw_final_kernel(const float* gXd, const void* gXp, float* gX,
+                                                       long long n) {
+    const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) gX[i] = gXd[i] + ld<T>(gXp, i);
+}
+
+template <typename T, int kD>
+hipError_t launch_dt(const BackwardArgs& a, hipStream_t s) {
+    const long long cells = (long long)a.G * a.G;
+    const long long n = (long long)a.B * cells * kHeads * kD;
+    hipLaunchKernelGGL((bw_loss_partial_kernel<T>), dim3(a.lchunks, a.B), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(bw_loss_finalize_kernel, dim3((a.B * kHeads + 63) / 64), dim3(64), 0, s, a);
+    hipLaunchKernelGGL((bw_cell_kernel<T, kD>), dim3(a.pods * kHeads * a.nW), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((bw_gather_kernel<T, kD>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(bw_param_finalize_kernel, dim3((a.pods * kHeads * kPartF + 63) / 64), dim3(64), 0,
+                       s, a);
+    if (a.per_cell)
+        hipLaunchKernelGGL(bw_cell_param_finalize_kernel,
+                           dim3((unsigned)((a.pods * cells * kHeads + 255) / 256)), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_t(const BackwardArgs& a, hipStream_t s) {
+    switch (a.D) {
+        case 8: return launch_dt<T, 8>(a, s);
+        case 16: return launch_dt<T, 16>(a, s);
+        case 32: return launch_dt<T, 32>(a, s);
+        case 64: return launch_dt<T, 64>(a, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace
+
+int backward_loss_chunks(int G) { return (G * G + kLossCells - 1) / kLossCells; }
+int backward_part_floats() { return kPartF; }
+int backward_dw_chunks_per_pod(long long rows_per_pod) { return (int)((rows_per_pod + kWRows - 1) / kWRows); }
+
+hipError_t launch_backward_stencil(int dtype, const BackwardArgs& a, hipStream_t s) {
+    return dtype == 1 ? launch_t<bf16_t>(a, s) : launch_t<float>(a, s);
+}
+
+hipError_t launch_backward_dw(int dtype, const BackwardArgs& a, const DwArgs& d, hipStream_t s) {
+    const dim3 grid(d.C / 64, 3 * d.C / 64, d.pods * d.chunks_per_pod);
+    if (dtype == 1)
+        hipLaunchKernelGGL((bw_dw_partial_kernel<bf16_t>), grid, dim3(256), 0, s, a, d);
+    else
+        hipLaunchKernelGGL((bw_dw_partial_kernel<float>), grid, dim3(256), 0, s, a, d);
+    const long long n = (long long)d.pods * d.C * 3 * d.C;
+    hipLaunchKernelGGL(bw_dw_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, d);
+    return hipGetLastError();
+}
+
+hipError_t launch_backward_final(int dtype, const float* gXd, const void* gXp, float* gX, long long n,
+                                 hipStream_t s) {
+    const dim3 grid((unsigned)((n + 255) / 256));
+    if (dtype == 1)
+        hipLaunchKernelGGL((bw_final_kernel<bf16_t>), grid, dim3(256), 0, s, gXd, gXp, gX, n);
+    else
+        hipLaunchKernelGGL((bw_final_kernel<float>), grid, dim3(256), 0, s, gXd, gXp, gX, n);
+    return hipGetLastError();
+}
+
+}  // namespace slime

@@ -92,6 +92,60 @@ struct FitnessArgs {
 int fitness_chunks(int G);
 hipError_t launch_fitness(int dtype, const FitnessArgs& a, hipStream_t s);
 
+// ---- backward of one step under the MSE loss (backward.hip) --------------------------------
+struct BackwardArgs {
+    // forward tape (one step from X, parallel projections, scale 1 on X)
+    const void* X;           // [B][G][G][C] input state (storage type)
+    const void* P;           // post-activation projections (storage type)
+    const void* I;
+    const void* V;
+    const void* Ipre;        // I before the GELU (storage type)
+    const float* Y;          // [B][G][G][C] unscaled step output, fp32
+    const void* T;           // target (storage type)
+    const float* scale;      // [B*H] conservation scale r
+    const float* K;          // parameters, layouts as StencilArgs
+    const float* mu;
+    const float* sigma;
+    const float* M;
+    int B, G, D, per_pod, pods, per_cell;
+    float dt;
+    float inv_n;             // 1 / (B G^2 C)
+    // work buffers
+    double* lpart;           // [B*H][lchunks][3]
+    int lchunks;             // backward_loss_chunks(G)
+    float* coef;             // [B*H][2]: gY = coef0 (gY' - coef1); coef1 also enters gX
+    double* loss_bh;         // [B*H] sum of squared errors
+    float* gU;               // [B][G][G][C] fp32
+    float* gVt;              // [B][G][G][C] fp32
+    float* att;              // [B][G][G][H][9] attention weights
+    float* gS;               // [B][G][G][H][9] score gradients
+    void* G3;                // [B][G][G][3C] gradients of P~, I~, V (storage type)
+    float* gXd;              // [B][G][G][C] direct part of dL/dX
+    float* ppart;            // [pods][H][nW][backward_part_floats()]
+    int nW;                  // workgroups per (pod, head) in the cell pass
+    float* gcell;            // per-cell growth: [B][G][G][H][2]
+    // outputs (device, fp32, parameter layouts; may be nullptr)
+    float* gK;
+    float* gmu;
+    float* gsigma;
+    float* gM;
+};
+struct DwArgs {
+    float* part;             // [pods * chunks_per_pod][C][3C]
+    int C, pods, chunks_per_pod;
+    long long rows_per_pod;
+    float* gWP;              // [pods][C][C] each, may be nullptr
+    float* gWI;
+    float* gWV;
+};
+int backward_loss_chunks(int G);
+int backward_part_floats();
+int backward_dw_chunks_per_pod(long long rows_per_pod);
+hipError_t launch_backward_stencil(int dtype, const BackwardArgs& a, hipStream_t s);
+hipError_t launch_backward_dw(int dtype, const BackwardArgs& a, const DwArgs& d, hipStream_t s);
+hipError_t launch_backward_final(int dtype, const float* gXd, const void* gXp, float* gX, long long n,
+                                 hipStream_t s);
+
 // ---- organism adapters (slime/core/organism.cu:691-743) -----------------------------
 hipError_t launch_init_from_field(int dtype, const float* conc, void* X, int G, int C,
                                   hipStream_t s);

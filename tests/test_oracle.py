@@ -392,3 +392,84 @@ def test_field_adapters(oracle):
 def test_oracle_reproduces_committed_golden(oracle):
     from tests.golden.make_golden import check_golden
     check_golden(oracle)
+
+
+# ---- backward (config c5's gradient): pinned by central finite differences -------------------
+# The analytic gradient of L = mean((step(X) - T)^2) is compared with
+# (L(x + e) - L(x - e)) / 2e of the oracle's own fp64 forward. Perturbations are
+# powers of two, exact in fp32 at these magnitudes, so the differences carry only
+# the O(e^2) truncation error. A dropped term, sign or transposed operand in any
+# stage's chain rule moves some sampled entry by far more than the tolerance.
+
+def _fd_entries(oracle, cfg, X, p, T, key, idxs, eps):
+    out = []
+    for idx in idxs:
+        hi = {k: v.copy() for k, v in p.items()}
+        lo = {k: v.copy() for k, v in p.items()}
+        xh, xl = X.copy(), X.copy()
+        if key == "X":
+            xh[idx] += eps
+            xl[idx] -= eps
+        else:
+            hi[key][idx] += eps
+            lo[key][idx] -= eps
+        out.append((oracle.step_loss(cfg, xh, hi, T) - oracle.step_loss(cfg, xl, lo, T)) / (2 * eps))
+    return np.array(out)
+
+
+@pytest.mark.parametrize("per_cell,pods,guard", [(False, 2, False), (True, 1, False), (False, 1, True)])
+def test_backward_matches_finite_differences(oracle, per_cell, pods, guard):
+    cfg = OracleConfig(B=2, G=6, H=H, D=4, pods=pods, growth_per_cell=per_cell)
+    p, X = _params(cfg, w_std=0.2), _state(cfg)
+    if guard:
+        p["M"][0, 3, :] = 0.0  # head 3's output is identically zero: the S7 guard path
+    T = _rng(9).random(X.shape, dtype=np.float32)
+    loss, gr = oracle.step_backward(cfg, X, p, T)
+    assert abs(loss - oracle.step_loss(cfg, X, p, T)) <= 1e-15 * max(loss, 1.0)
+    r = _rng(11)
+    checks = {
+        "X": (2.0 ** -10, [tuple(r.integers(0, s) for s in X.shape) for _ in range(16)]),
+        "WP": (2.0 ** -10, [tuple(r.integers(0, s) for s in p["WP"].shape) for _ in range(6)]),
+        "WI": (2.0 ** -10, [tuple(r.integers(0, s) for s in p["WI"].shape) for _ in range(6)]),
+        "WV": (2.0 ** -10, [tuple(r.integers(0, s) for s in p["WV"].shape) for _ in range(6)]),
+        "K": (2.0 ** -12, [tuple(r.integers(0, s) for s in p["K"].shape) for _ in range(6)]),
+        "mu": (2.0 ** -14, [tuple(r.integers(0, s) for s in p["mu"].shape) for _ in range(4)]),
+        "sigma": (2.0 ** -16, [tuple(r.integers(0, s) for s in p["sigma"].shape) for _ in range(4)]),
+        "M": (2.0 ** -12, [tuple(r.integers(0, s) for s in p["M"].shape) for _ in range(6)]),
+    }
+    if guard:
+        # Perturbing the zeroed row lifts |sum Y_3| above the guard, where the
+        # conserved output no longer depends on that row's scale: the loss is
+        # discontinuous there, so only entries off that row are differenced.
+        checks["M"] = (2.0 ** -12, [(0, o, h) for o, h in ((0, 3), (1, 5), (4, 4), (7, 2))])
+    for key, (eps, idxs) in checks.items():
+        fd = _fd_entries(oracle, cfg, X, p, T, key, idxs, eps)
+        an = np.array([gr[key][i] for i in idxs], dtype=np.float64)
+        scale = np.max(np.abs(gr[key]))
+        assert scale > 0, key
+        np.testing.assert_allclose(an, fd, rtol=2e-3, atol=2e-4 * scale, err_msg=key)
+
+
+def test_backward_dt_zero_is_conserved_linear_map(oracle):
+    # dt = 0 and M = I: Y = X exactly with scale 1, so L = mean((X - T)^2). The
+    # conservation terms cancel (gY = gY' - Q/B through Y, + Q/B through the input
+    # mass), leaving dL/dX = 2 (X - T) / N.
+    cfg = OracleConfig(B=1, G=5, H=H, D=2, dt=0.0)
+    p, X = _params(cfg), _state(cfg)
+    p["M"] = np.eye(H, dtype=np.float32)[None]
+    T = _rng(5).random(X.shape, dtype=np.float32)
+    loss, gr = oracle.step_backward(cfg, X, p, T)
+    N = X.size
+    Xd, Td = X.astype(np.float64), T.astype(np.float64)
+    assert abs(loss - np.mean((Xd - Td) ** 2)) <= 1e-12
+    np.testing.assert_allclose(gr["X"], 2 * (Xd - Td) / N, rtol=1e-5, atol=1e-9)
+    # with dt = 0 nothing depends on the projections, the potential or the growth
+    for k in ("WP", "WI", "WV", "K", "mu", "sigma"):
+        assert np.all(gr[k] == 0), k
+
+
+def test_backward_rejects_chained_projections(oracle):
+    cfg = OracleConfig(B=1, G=4, H=H, D=2, pvi_chain=True)
+    p, X = _params(cfg), _state(cfg)
+    with pytest.raises(ValueError):
+        oracle.step_backward(cfg, X, p, X)
