@@ -91,6 +91,10 @@ def main() -> int:
     ap.add_argument("--config", default="c3")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--backward", action="store_true",
+                    help="time the c5 gradient (slime_ca_backward) instead of the headline")
+    ap.add_argument("--ensemble", action="store_true",
+                    help="time the c4 ensemble: 16 pods' steps and the fused fitness")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported in this "
@@ -103,6 +107,10 @@ def main() -> int:
 
     from slime_amd import CONFIGS, Pseudopod, make_params, make_state
 
+    if args.backward:
+        return bench_backward(args)
+    if args.ensemble:
+        return bench_ensemble(args)
     cfg = CONFIGS[args.config]
     log(f"config {cfg}")
     params = make_params(cfg, seed=1)
@@ -189,6 +197,92 @@ def main() -> int:
         "mass_drift_max": drift, "finite": finite,
         "roofline": roofline, "kernels": kernels, "cpu_baseline": cpu,
     }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def _time(fn, reps: int):
+    import torch
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / reps * 1e3
+
+
+def bench_backward(args) -> int:
+    """c5: one forward step plus the gradient of the MSE loss,
+    with and without the weight gradients; prints one JSON line."""
+    import numpy as np
+    import torch
+
+    from slime_amd import CONFIGS, Pseudopod, make_params, make_state
+    cfg = CONFIGS["c5"]
+    log(f"config {cfg}")
+    p = make_params(cfg, seed=1)
+    x = torch.from_numpy(make_state(cfg, seed=2)).to("cuda").to(torch.bfloat16).contiguous()
+    t = torch.rand(x.shape, generator=torch.Generator().manual_seed(3)).to("cuda").to(torch.bfloat16)
+    with Pseudopod(cfg.B, cfg.G, cfg.H, cfg.D, cfg.dtype, cfg.dt, False, 1) as ca:
+        ca.set_params(p)
+        y = torch.empty_like(x)
+        ca.forward(x, out=y)
+        ca.backward(x, t)
+        reps = max(args.steps // 2, 1)
+        fwd = _time(lambda: ca.forward(x, out=y), reps)
+        bwd_x = _time(lambda: ca.backward(x, t, params=False), reps)
+        bwd = _time(lambda: ca.backward(x, t, params=True), reps)
+        loss, _, _ = ca.backward(x, t, params=False)
+    cells = cfg.cell_updates_per_step
+    out = {"metric": "c5 forward + gradient time (512x512, 8 heads, d=64, batch 4, bf16)",
+           "unit": "ms", "higher_is_better": False, "n_gpus": 1, "dtype": cfg.dtype,
+           "data": "synthetic: seeded U[0,1) state with 5% blobs, U[0,1) target",
+           "config": {"workload": "c5", "grid": cfg.G, "batch": cfg.B, "heads": cfg.H,
+                      "head_dim": cfg.D},
+           "forward_ms": fwd, "backward_dx_ms": bwd_x, "backward_all_ms": bwd,
+           "cell_updates_per_s_backward_dx": cells / (bwd_x * 1e-3), "loss": loss, "reps": reps}
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def bench_ensemble(args) -> int:
+    """c4: 16 pods with independent weights, batch entry = pod,
+    8 steps, then the fused fitness over the 8-state history; prints one JSON line."""
+    import torch
+
+    from slime_amd import CONFIGS, Pseudopod, make_params, make_state
+    cfg = CONFIGS["c4"]
+    log(f"config {cfg}")
+    p = make_params(cfg, seed=1)
+    x0 = torch.from_numpy(make_state(cfg, seed=2, B=1)).to("cuda").to(torch.bfloat16)
+    x0 = x0.expand(cfg.B, -1, -1, -1).contiguous()  # shared initial grid
+    T = cfg.steps
+    with Pseudopod(cfg.B, cfg.G, cfg.H, cfg.D, cfg.dtype, cfg.dt, False, cfg.pods) as ca:
+        ca.set_params(p)
+        hist = torch.empty((T,) + tuple(x0.shape), dtype=torch.bfloat16, device="cuda")
+
+        def rollout():
+            hist[0].copy_(x0)
+            for i in range(1, T):
+                ca.forward(hist[i - 1], out=hist[i])
+
+        rollout()
+        ca.fitness(hist)
+        reps = max(args.steps // 2, 1)
+        roll_ms = _time(rollout, reps)
+        fit_ms = _time(lambda: ca.fitness(hist), reps * 4)
+        er, coh, fit = ca.fitness(hist)
+        torch.cuda.synchronize()
+    steps = T - 1
+    out = {"metric": "c4 ensemble: step throughput and fused fitness latency",
+           "unit": "cell-updates/s", "higher_is_better": True, "n_gpus": 1, "dtype": cfg.dtype,
+           "data": "synthetic: 16 pods of seeded weights on one shared seeded grid",
+           "config": {"workload": "c4", "pods": cfg.pods, "grid": cfg.G, "batch": cfg.B,
+                      "history": T},
+           "value": cfg.cell_updates_per_step * steps / (roll_ms * 1e-3),
+           "rollout_ms": roll_ms, "steps": steps, "fitness_us": fit_ms * 1e3,
+           "fitness_mean": float(fit.mean()), "erank_mean": float(er.mean()),
+           "coherence_mean": float(coh.mean())}
     print(json.dumps(out), flush=True)
     return 0
 

@@ -1,4 +1,5 @@
-"""Builds ``slime_amd/libslime_ca.so`` (the HIP kernels + C ABI) for gfx950.
+"""Builds ``slime_amd/libslime_ca.so`` (the HIP kernels + C ABI) for gfx950, and
+``slime_amd/libslime_probe.so`` (the ceiling measurements of ``calibrate.py``).
 
 Each source is compiled with hipcc in parallel into ``slime_amd/_build/`` and
 linked into one shared library next to this file. Packed-fp32 instructions are
@@ -19,6 +20,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libslime_ca.so")
+PROBE_LIB = os.path.join(HERE, "libslime_probe.so")  # measured ceilings (calibrate.py)
 SOURCES = ["api.cpp", "gemm.hip", "stencil.hip", "mass.hip", "fitness.hip", "organism.hip",
            "backward.hip"]
 ARCH = "gfx950"
@@ -56,8 +58,14 @@ def build(verbose: bool = False) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
     os.replace(tmp, LIB)
+    tmp = PROBE_LIB + ".tmp"
+    cmd = [hipcc(), *flags(), "-x", "hip", "-shared", os.path.join(CSRC, "probe.hip"), "-o", tmp]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed for probe.hip:\n{r.stderr}")
+    os.replace(tmp, PROBE_LIB)
     if verbose:
-        print(f"built {LIB}")
+        print(f"built {LIB} and {PROBE_LIB}")
     return LIB
 
 

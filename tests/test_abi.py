@@ -69,3 +69,15 @@ def test_valid_config_without_gpu_reports_no_device():
     rc = lib.slime_ca_create(ctypes.byref(_cfg()), ctypes.byref(h))
     assert rc in (_lib.SLIME_ENODEV, _lib.SLIME_EHIP)
     assert not h.value
+
+
+def test_probe_library_exports_the_ceiling_probes():
+    """libslime_probe.so (measured MFMA/HBM ceilings) is separate from the CA library."""
+    path = os.path.join(ROOT, "slime_amd", "libslime_probe.so")
+    if not os.path.exists(path):
+        pytest.skip("probe library not built")
+    lib = ctypes.CDLL(path)
+    assert hasattr(lib, "slime_probe_mfma_tflops")
+    assert hasattr(lib, "slime_probe_hbm_gbs")
+    ca = _lib.load()
+    assert not hasattr(ca, "slime_probe_mfma_tflops")
