@@ -1,6 +1,6 @@
 """Benchmark: CA cell-updates/s of the multi-head neural-CA step on one MI355X.
 
-Workload (BASELINE configs[2], "c3"): 128x128 toroidal grid, 8 heads, head_dim 64,
+Workload ("c3"): 128x128 toroidal grid, 8 heads, head_dim 64,
 batch 64, bf16 state and weights with fp32 accumulation, synthetic seeded input
 resident in HBM. One step = S1 projections ([P|I|V] GEMM, 1,048,576 x 512 x 1536)
 + the fused stencil (S2-S6) + mass conservation (S7) over the whole batch; one
@@ -98,7 +98,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported in this "
-              "build (the path shards by batch with no collective; see DESIGN.md)",
+              "build (the path shards by batch with no collective)",
               file=sys.stderr)
         return 2
 
@@ -212,7 +212,7 @@ def _time(fn, reps: int):
 
 
 def bench_backward(args) -> int:
-    """c5 (BASELINE configs[4]): one forward step plus the gradient of the MSE loss,
+    """c5: one forward step plus the gradient of the MSE loss,
     with and without the weight gradients; prints one JSON line."""
     import numpy as np
     import torch
@@ -246,7 +246,7 @@ def bench_backward(args) -> int:
 
 
 def bench_ensemble(args) -> int:
-    """c4 (BASELINE configs[3]): 16 pods with independent weights, batch entry = pod,
+    """c4: 16 pods with independent weights, batch entry = pod,
     8 steps, then the fused fitness over the 8-state history; prints one JSON line."""
     import torch
 

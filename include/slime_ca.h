@@ -134,7 +134,7 @@ typedef struct {
 } slime_ca_grads;
 
 /* One step from x_in (parallel projections) and the gradient of the loss
- * L = mean((x_out - target)^2) over all B*G*G*C elements,
+ * L = mean((x_out - target)^2) over all B*G*G*C elements (configuration c5),
  * x_out taken before its storage rounding: grad_x (device fp32 [B][G][G][C])
  * and, through grads (may be NULL), the parameter gradients. *loss (host, may be
  * NULL) receives L, which synchronises the stream. No counterpart in the

@@ -1,4 +1,4 @@
-"""GPU backward (slime_ca_backward): the gradient of
+"""GPU backward (slime_ca_backward, configuration c5): the gradient of
 L = mean((step(X) - T)^2) against the CPU oracle's fp64 gradient (itself pinned by
 finite differences in tests/test_oracle.py), and at the c5 shape against central
 finite differences of an independent fp64 numpy forward on 64 sampled cells.
