@@ -189,6 +189,71 @@ int slime_ca_set_timing(slime_ca* ca, int enable);
 int slime_ca_timings(slime_ca* ca, double* gemm_ms, int* gemm_launches, double* stencil_ms,
                      int* stencil_launches);
 
+/* ---- fitness consumers: the component pool -----------------------------------------
+ * The reference's ComponentPool / PoolEntry (slime/memory/pool.cu:12-30) as a
+ * structure of device arrays owned by the caller (nothing is allocated by these
+ * calls). counters = {active_count, total_spawned, total_culled}. */
+typedef struct {
+    int capacity;      /* entries (MAX_POOL_SIZE = 256 in the reference) */
+    int genome_size;   /* floats per genome (GENOME_SIZE = 512) */
+    int* id;           /* [capacity] */
+    float* fitness;    /* [capacity] */
+    float* coherence;  /* [capacity] */
+    float* hunger;     /* [capacity] */
+    int* age;          /* [capacity] */
+    int* alive;        /* [capacity], 0 or 1 */
+    float* genome;     /* [capacity][genome_size] */
+    float* gradients;  /* [capacity][genome_size] */
+    int* counters;     /* [3]: active, spawned, culled */
+} slime_pool;
+
+/* Every entry dead with id -1, fitness 0, coherence 0, hunger 0.5, age 0, zero
+ * genome and gradients; counters 0. Replaces init_pool_kernel
+ * (slime/memory/pool.cu:300-320). */
+int slime_pool_init(const slime_pool* pool, void* stream);
+
+/* Alive entry i < n takes fitness = mean over `heads` of fitness[i*heads + h],
+ * coherence likewise, hunger = 1 - coherence, and fitness_history /
+ * coherence_history[generation * capacity + i] (either may be NULL). With the
+ * per-(batch, head) outputs of slime_ca_fitness and batch entry = component, this
+ * feeds the fused CA fitness to the pool in place of the genome-norm proxy of
+ * fitness_computation_kernel (slime/core/organism.cu:204-289). */
+int slime_pool_set_fitness(const slime_pool* pool, const float* fitness, const float* coherence, int n,
+                           int heads, int generation, float* fitness_history,
+                           float* coherence_history, void* stream);
+
+/* hunger[i] = 1 - coherence[i] over n device floats: hunger_kernel
+ * (slime/kernels/warp_ca.cu:229-240). */
+int slime_ca_hunger(const float* coherence, float* hunger, int n, void* stream);
+
+/* age += 1 for alive entries: age_components_kernel (slime/memory/pool.cu:162-168). */
+int slime_pool_age(const slime_pool* pool, void* stream);
+
+/* An alive entry dies when fitness < fitness_threshold * 0.1 or hunger >
+ * hunger_threshold (active -1, culled +1 each): culling_kernel
+ * (slime/core/organism.cu:590-614; the lifecycle passes 0.8 and 0.95). */
+int slime_pool_cull(const slime_pool* pool, float fitness_threshold, float hunger_threshold,
+                    void* stream);
+
+/* One spawn into the first dead slot when active < capacity: spawn_component_kernel
+ * (slime/memory/pool.cu:57-121). parent outside [0, capacity) draws a uniform
+ * genome in [-1, 1). */
+int slime_pool_spawn(const slime_pool* pool, int parent, float mutation_rate, void* stream);
+
+/* The spawn wave of the lifecycle (slime/core/organism.cu:557-587): 32 draws in
+ * lane order, each spawning from the first alive entry with fitness > 0.5 (rate
+ * 0.01) when the draw is below `probability`. probability < 0 computes the
+ * lifecycle's 0.1 * exp(-active / 256) on the device and skips the wave unless it
+ * exceeds 0.01 (organism.cu:185-186). */
+int slime_pool_spawn_wave(const slime_pool* pool, float probability, int generation, void* stream);
+
+/* The fitness consumers of one lifecycle generation (component_evolution_kernel,
+ * slime/core/organism.cu:144-201, without selection and archive): set_fitness,
+ * spawn wave with the device-computed probability, cull at 0.8 / 0.95. */
+int slime_pool_evolve(const slime_pool* pool, const float* fitness, const float* coherence, int n,
+                      int heads, int generation, float* fitness_history, float* coherence_history,
+                      void* stream);
+
 /* 1 when this build runs S1 on the MFMA tile kernel for the handle's shape. */
 int slime_ca_uses_mfma(const slime_ca* ca);
 

@@ -245,3 +245,100 @@ def field_from_state(X):
 
 def num_threads() -> int:
     return lib().oracle_num_threads()
+
+
+# ---- component pool (pool_oracle.cpp) -------------------------------------------------
+class _PoolC(ctypes.Structure):
+    _fields_ = [("capacity", ctypes.c_int), ("genome_size", ctypes.c_int)] + [
+        (n, ctypes.c_void_p) for n in ("id", "fitness", "coherence", "hunger", "age", "alive",
+                                       "genome", "gradients", "counters")]
+
+
+class Pool:
+    """Host component pool in the layout of ``slime_pool`` (numpy arrays); the
+    methods run the oracle's restatement of the reference's pool kernels."""
+
+    FIELDS = ("id", "fitness", "coherence", "hunger", "age", "alive", "genome", "gradients", "counters")
+
+    def __init__(self, capacity: int = 256, genome_size: int = 512):
+        self.capacity, self.genome_size = capacity, genome_size
+        self.id = np.full(capacity, -1, np.int32)
+        self.fitness = np.zeros(capacity, np.float32)
+        self.coherence = np.zeros(capacity, np.float32)
+        self.hunger = np.full(capacity, 0.5, np.float32)
+        self.age = np.zeros(capacity, np.int32)
+        self.alive = np.zeros(capacity, np.int32)
+        self.genome = np.zeros((capacity, genome_size), np.float32)
+        self.gradients = np.zeros((capacity, genome_size), np.float32)
+        self.counters = np.zeros(3, np.int32)
+
+    def _c(self) -> _PoolC:
+        return _PoolC(self.capacity, self.genome_size, *[getattr(self, n).ctypes.data for n in self.FIELDS])
+
+    def copy(self) -> "Pool":
+        q = Pool(self.capacity, self.genome_size)
+        for n in self.FIELDS:
+            setattr(q, n, getattr(self, n).copy())
+        return q
+
+    def init(self) -> None:
+        lib().oracle_pool_init(ctypes.byref(self._c()))
+
+    def set_fitness(self, fitness, coherence, n: int, heads: int, generation: int,
+                    fitness_history=None, coherence_history=None) -> None:
+        f, c = _f32(fitness), _f32(coherence)
+        fh = fitness_history.ctypes.data if fitness_history is not None else None
+        ch = coherence_history.ctypes.data if coherence_history is not None else None
+        lib().oracle_pool_set_fitness(ctypes.byref(self._c()), _p(f), _p(c), n, heads, generation,
+                                      ctypes.c_void_p(fh), ctypes.c_void_p(ch))
+
+    def age_up(self) -> None:
+        lib().oracle_pool_age(ctypes.byref(self._c()))
+
+    def cull(self, fitness_threshold: float, hunger_threshold: float) -> None:
+        lib().oracle_pool_cull(ctypes.byref(self._c()), ctypes.c_float(fitness_threshold),
+                               ctypes.c_float(hunger_threshold))
+
+    def spawn(self, parent: int, rate: float) -> None:
+        lib().oracle_pool_spawn(ctypes.byref(self._c()), parent, ctypes.c_float(rate))
+
+    def spawn_wave(self, probability: float, generation: int) -> float:
+        fn = lib().oracle_pool_spawn_wave
+        fn.restype = ctypes.c_float
+        return fn(ctypes.byref(self._c()), ctypes.c_float(probability), generation)
+
+    def evolve(self, fitness, coherence, n: int, heads: int, generation: int,
+               fitness_history=None, coherence_history=None) -> None:
+        f, c = _f32(fitness), _f32(coherence)
+        fh = fitness_history.ctypes.data if fitness_history is not None else None
+        ch = coherence_history.ctypes.data if coherence_history is not None else None
+        lib().oracle_pool_evolve(ctypes.byref(self._c()), _p(f), _p(c), n, heads, generation,
+                                 ctypes.c_void_p(fh), ctypes.c_void_p(ch))
+
+
+def hunger(coherence) -> np.ndarray:
+    c = _f32(coherence)
+    out = np.empty_like(c)
+    lib().oracle_hunger(_p(c), _p(out), c.size)
+    return out
+
+
+class Xorshift128p:
+    """The oracle's xorshift128+ stream (float mapping and Box-Muller of the reference)."""
+
+    def __init__(self, s0: int, s1: int):
+        self.s = (ctypes.c_ulonglong * 2)(s0 & (2**64 - 1), s1 & (2**64 - 1))
+
+    def next(self) -> float:
+        fn = lib().oracle_xorshift_next
+        fn.restype = ctypes.c_float
+        return fn(ctypes.byref(self.s, 0), ctypes.byref(self.s, 8))
+
+    def gaussian(self) -> float:
+        fn = lib().oracle_xorshift_gaussian
+        fn.restype = ctypes.c_float
+        return fn(ctypes.byref(self.s, 0), ctypes.byref(self.s, 8))
+
+    @property
+    def state(self) -> tuple:
+        return int(self.s[0]), int(self.s[1])

@@ -70,6 +70,32 @@ int oracle_field_from_state(int G, int C, const float* X, float* conc);
 
 int oracle_num_threads(void);
 
+/* Component pool (pool_oracle.cpp): host arrays in the layout of slime_pool. */
+typedef struct {
+    int capacity, genome_size;
+    int* id;
+    float* fitness;
+    float* coherence;
+    float* hunger;
+    int* age;
+    int* alive;
+    float* genome;    /* [capacity][genome_size] */
+    float* gradients; /* [capacity][genome_size] */
+    int* counters;    /* active, spawned, culled */
+} oracle_pool;
+float oracle_xorshift_next(unsigned long long* s0, unsigned long long* s1);
+float oracle_xorshift_gaussian(unsigned long long* s0, unsigned long long* s1);
+void oracle_pool_init(oracle_pool* p);
+void oracle_pool_set_fitness(oracle_pool* p, const float* fit, const float* coh, int n, int heads,
+                             int generation, float* fit_hist, float* coh_hist);
+void oracle_hunger(const float* coh, float* hunger, int n);
+void oracle_pool_age(oracle_pool* p);
+void oracle_pool_cull(oracle_pool* p, float fitness_threshold, float hunger_threshold);
+void oracle_pool_spawn(oracle_pool* p, int parent, float rate);
+float oracle_pool_spawn_wave(oracle_pool* p, float probability, int generation);
+void oracle_pool_evolve(oracle_pool* p, const float* fit, const float* coh, int n, int heads,
+                        int generation, float* fit_hist, float* coh_hist);
+
 #ifdef __cplusplus
 }
 #endif

@@ -8,5 +8,6 @@ so ``python -m slime_amd.build`` can run before it exists.)
 """
 from ._lib import SlimeError, load  # noqa: F401
 from .ca import Pseudopod  # noqa: F401
+from .pool import ComponentPool  # noqa: F401
 from .synthetic import CONFIGS, CAConfig, make_params, make_state, round_bf16  # noqa: F401
 

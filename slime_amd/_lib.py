@@ -25,7 +25,9 @@ EXPORTS = (
     "slime_ca_flow_lenia", "slime_ca_step", "slime_ca_mass", "slime_ca_fitness",
     "slime_ca_fitness_sweeps", "slime_ca_init_from_field", "slime_ca_field_from_state",
     "slime_ca_uses_mfma", "slime_ca_set_timing", "slime_ca_timings", "slime_ca_last_error",
-    "slime_neural_ca_update", "slime_ca_backward",
+    "slime_neural_ca_update", "slime_ca_backward", "slime_pool_init", "slime_pool_set_fitness",
+    "slime_ca_hunger", "slime_pool_age", "slime_pool_cull", "slime_pool_spawn", "slime_pool_spawn_wave",
+    "slime_pool_evolve",
 )
 
 
@@ -49,6 +51,13 @@ class MultiHeadCAState(ctypes.Structure):
 class Grads(ctypes.Structure):
     """slime_ca_grads: device fp32 parameter-gradient pointers (NULL allowed)."""
     _fields_ = [(n, ctypes.c_void_p) for n in ("WP", "WI", "WV", "K", "mu", "sigma", "M")]
+
+
+class Pool(ctypes.Structure):
+    """slime_pool: device arrays of the component pool."""
+    _fields_ = [("capacity", ctypes.c_int), ("genome_size", ctypes.c_int)] + [
+        (n, ctypes.c_void_p) for n in ("id", "fitness", "coherence", "hunger", "age", "alive",
+                                       "genome", "gradients", "counters")]
 
 
 class SlimeError(RuntimeError):
@@ -88,12 +97,19 @@ def load() -> ctypes.CDLL:
         "slime_neural_ca_update": [vp, ctypes.POINTER(MultiHeadCAState), vp, vp, i, vp],
         "slime_ca_backward": [vp, vp, vp, vp, ctypes.POINTER(Grads), ctypes.POINTER(ctypes.c_double),
                               vp],
+        "slime_pool_init": [ctypes.POINTER(Pool), vp],
+        "slime_pool_set_fitness": [ctypes.POINTER(Pool), vp, vp, i, i, i, vp, vp, vp],
+        "slime_ca_hunger": [vp, vp, i, vp],
+        "slime_pool_age": [ctypes.POINTER(Pool), vp],
+        "slime_pool_cull": [ctypes.POINTER(Pool), f, f, vp],
+        "slime_pool_spawn": [ctypes.POINTER(Pool), i, f, vp],
+        "slime_pool_spawn_wave": [ctypes.POINTER(Pool), f, i, vp],
+        "slime_pool_evolve": [ctypes.POINTER(Pool), vp, vp, i, i, i, vp, vp, vp],
     }
     for name, args in sig.items():
         fn = getattr(lib, name)
         fn.argtypes = args
         fn.restype = ctypes.c_char_p if name == "slime_ca_last_error" else ip
-    del f
     _lib = lib
     return lib
 

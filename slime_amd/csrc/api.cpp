@@ -793,6 +793,94 @@ int slime_ca_timings(slime_ca* h, double* gemm_ms, int* gemm_n, double* stencil_
     return sum(h->stencil_ev, stencil_ms, stencil_n);
 }
 
+// ---- component pool -------------------------------------------------------------------
+static int pool_args(const slime_pool* p, PoolArgs* a) {
+    if (!p) return fail(SLIME_EINVAL, "pool is NULL");
+    if (p->capacity <= 0 || p->genome_size <= 0)
+        return fail(SLIME_EINVAL, "pool capacity %d and genome_size %d must be positive", p->capacity,
+                    p->genome_size);
+    if (!p->id || !p->fitness || !p->coherence || !p->hunger || !p->age || !p->alive || !p->genome ||
+        !p->gradients || !p->counters)
+        return fail(SLIME_EINVAL, "a pool array is NULL");
+    *a = PoolArgs{p->capacity, p->genome_size, p->id, p->fitness, p->coherence, p->hunger,
+                  p->age, p->alive, p->genome, p->gradients, p->counters};
+    return SLIME_OK;
+}
+
+int slime_pool_init(const slime_pool* pool, void* stream) {
+    PoolArgs a;
+    if (int rc = pool_args(pool, &a)) return rc;
+    HIP_TRY(launch_pool_init(a, (hipStream_t)stream));
+    return SLIME_OK;
+}
+
+int slime_pool_set_fitness(const slime_pool* pool, const float* fitness, const float* coherence, int n,
+                           int heads, int generation, float* fitness_history,
+                           float* coherence_history, void* stream) {
+    PoolArgs a;
+    if (int rc = pool_args(pool, &a)) return rc;
+    if (!fitness || !coherence) return fail(SLIME_EINVAL, "fitness or coherence is NULL");
+    if (n < 0 || heads <= 0 || generation < 0)
+        return fail(SLIME_EINVAL, "n %d, heads %d and generation %d must be >= 0, > 0, >= 0", n, heads,
+                    generation);
+    if (n == 0) return SLIME_OK;
+    HIP_TRY(launch_pool_set_fitness(a, fitness, coherence, n, heads, generation, fitness_history,
+                                    coherence_history, (hipStream_t)stream));
+    return SLIME_OK;
+}
+
+int slime_ca_hunger(const float* coherence, float* hunger, int n, void* stream) {
+    if (n < 0) return fail(SLIME_EINVAL, "n %d < 0", n);
+    if (n == 0) return SLIME_OK;
+    if (!coherence || !hunger) return fail(SLIME_EINVAL, "coherence or hunger is NULL");
+    HIP_TRY(launch_hunger(coherence, hunger, n, (hipStream_t)stream));
+    return SLIME_OK;
+}
+
+int slime_pool_age(const slime_pool* pool, void* stream) {
+    PoolArgs a;
+    if (int rc = pool_args(pool, &a)) return rc;
+    HIP_TRY(launch_pool_age(a, (hipStream_t)stream));
+    return SLIME_OK;
+}
+
+int slime_pool_cull(const slime_pool* pool, float fitness_threshold, float hunger_threshold,
+                    void* stream) {
+    PoolArgs a;
+    if (int rc = pool_args(pool, &a)) return rc;
+    if (!std::isfinite(fitness_threshold) || !std::isfinite(hunger_threshold))
+        return fail(SLIME_EINVAL, "cull thresholds must be finite");
+    HIP_TRY(launch_pool_cull(a, fitness_threshold, hunger_threshold, (hipStream_t)stream));
+    return SLIME_OK;
+}
+
+int slime_pool_spawn(const slime_pool* pool, int parent, float mutation_rate, void* stream) {
+    PoolArgs a;
+    if (int rc = pool_args(pool, &a)) return rc;
+    if (!std::isfinite(mutation_rate)) return fail(SLIME_EINVAL, "mutation_rate must be finite");
+    HIP_TRY(launch_pool_spawn(a, parent, mutation_rate, (hipStream_t)stream));
+    return SLIME_OK;
+}
+
+int slime_pool_spawn_wave(const slime_pool* pool, float probability, int generation, void* stream) {
+    PoolArgs a;
+    if (int rc = pool_args(pool, &a)) return rc;
+    if (std::isnan(probability) || generation < 0)
+        return fail(SLIME_EINVAL, "probability is NaN or generation %d < 0", generation);
+    HIP_TRY(launch_pool_spawn_wave(a, probability, generation, (hipStream_t)stream));
+    return SLIME_OK;
+}
+
+int slime_pool_evolve(const slime_pool* pool, const float* fitness, const float* coherence, int n,
+                      int heads, int generation, float* fitness_history, float* coherence_history,
+                      void* stream) {
+    if (int rc = slime_pool_set_fitness(pool, fitness, coherence, n, heads, generation, fitness_history,
+                                        coherence_history, stream))
+        return rc;
+    if (int rc = slime_pool_spawn_wave(pool, -1.0f, generation, stream)) return rc;
+    return slime_pool_cull(pool, 0.8f, 0.95f, stream);
+}
+
 int slime_ca_uses_mfma(const slime_ca* h) {
     if (!h) return 0;
     const slime_ca_config& c = h->cfg;

@@ -154,4 +154,26 @@ hipError_t launch_field_from_state(int dtype, const void* X, float* conc, int G,
 hipError_t launch_organism_report(const double* mass_out, const float* erank, int H,
                                   float* mass_buffer, float* erank_out, hipStream_t s);
 
+// ---- component pool (slime_pool; slime/memory/pool.cu, slime/core/organism.cu) --------
+struct PoolArgs {
+    int capacity, genome_size;
+    int* id;
+    float* fitness;
+    float* coherence;
+    float* hunger;
+    int* age;
+    int* alive;
+    float* genome;     // [capacity][genome_size]
+    float* gradients;  // [capacity][genome_size]
+    int* counters;     // active, spawned, culled
+};
+hipError_t launch_pool_init(const PoolArgs& p, hipStream_t s);
+hipError_t launch_pool_set_fitness(const PoolArgs& p, const float* fit, const float* coh, int n, int heads,
+                                   int generation, float* fit_hist, float* coh_hist, hipStream_t s);
+hipError_t launch_hunger(const float* coh, float* hunger, int n, hipStream_t s);
+hipError_t launch_pool_age(const PoolArgs& p, hipStream_t s);
+hipError_t launch_pool_cull(const PoolArgs& p, float fitness_threshold, float hunger_threshold, hipStream_t s);
+hipError_t launch_pool_spawn(const PoolArgs& p, int parent, float rate, hipStream_t s);
+hipError_t launch_pool_spawn_wave(const PoolArgs& p, float probability, int generation, hipStream_t s);
+
 }  // namespace slime
