@@ -254,6 +254,23 @@ int slime_pool_evolve(const slime_pool* pool, const float* fitness, const float*
                       int heads, int generation, float* fitness_history, float* coherence_history,
                       void* stream);
 
+/* One generation record of the reference's evolution.json (extract_system_state,
+ * slime/extract_state.cu:64-184), written into buf (NUL-terminated):
+ *   {"gen":G,"elapsed":E.EE,"chemical":{"concentration":[16x16 centre sample, %.4f],
+ *    "size":16},"ca":{"flow_kernels":[[9 x %.4f] per head]},"agents":[],"voronoi":[],
+ *    "archive":{"size":0,"elites":[]},"pool":{"active":A,"capacity":C,"spawned":S,
+ *    "culled":K}}
+ * with the keys in the reference's order. chemical_concentration is device [G][G]
+ * fp32 (the sample is min(16, G) wide, centred); flow_kernels are pod 0's K of the
+ * handle; pool (may be NULL: zeros) supplies the counters. The behavioural agents,
+ * Voronoi cells and elite archive have no counterpart here and are written empty,
+ * so the record stays valid JSON (the reference's archive object closes one brace
+ * too many). *written receives the record's length; a buffer shorter than that
+ * plus its NUL is SLIME_EINVAL. Synchronous, like the reference's extraction. */
+int slime_snapshot_json(const slime_ca* ca, const float* chemical_concentration,
+                        const slime_pool* pool, int generation, double elapsed, char* buf,
+                        size_t cap, size_t* written);
+
 /* 1 when this build runs S1 on the MFMA tile kernel for the handle's shape. */
 int slime_ca_uses_mfma(const slime_ca* ca);
 

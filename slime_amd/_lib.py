@@ -27,7 +27,7 @@ EXPORTS = (
     "slime_ca_uses_mfma", "slime_ca_set_timing", "slime_ca_timings", "slime_ca_last_error",
     "slime_neural_ca_update", "slime_ca_backward", "slime_pool_init", "slime_pool_set_fitness",
     "slime_ca_hunger", "slime_pool_age", "slime_pool_cull", "slime_pool_spawn", "slime_pool_spawn_wave",
-    "slime_pool_evolve",
+    "slime_pool_evolve", "slime_snapshot_json",
 )
 
 
@@ -105,6 +105,8 @@ def load() -> ctypes.CDLL:
         "slime_pool_spawn": [ctypes.POINTER(Pool), i, f, vp],
         "slime_pool_spawn_wave": [ctypes.POINTER(Pool), f, i, vp],
         "slime_pool_evolve": [ctypes.POINTER(Pool), vp, vp, i, i, i, vp, vp, vp],
+        "slime_snapshot_json": [vp, vp, ctypes.POINTER(Pool), i, ctypes.c_double, ctypes.c_char_p,
+                                ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)],
     }
     for name, args in sig.items():
         fn = getattr(lib, name)

@@ -881,6 +881,51 @@ int slime_pool_evolve(const slime_pool* pool, const float* fitness, const float*
     return slime_pool_cull(pool, 0.8f, 0.95f, stream);
 }
 
+int slime_snapshot_json(const slime_ca* h, const float* conc, const slime_pool* pool, int generation,
+                        double elapsed, char* buf, size_t cap, size_t* written) {
+    if (!h || !conc || !written) return fail(SLIME_EINVAL, "NULL handle, field or length pointer");
+    if (!h->params_set) return fail(SLIME_ESTATE, "parameters not set");
+    if (!std::isfinite(elapsed)) return fail(SLIME_EINVAL, "elapsed is not finite");
+    const slime_ca_config& c = h->cfg;
+    HIP_TRY(hipSetDevice(h->device));
+    const int n = c.G < 16 ? c.G : 16, off = (c.G - n) / 2;
+    std::vector<float> sample((size_t)n * n), K((size_t)c.H * 9);
+    HIP_TRY(hipMemcpy2D(sample.data(), n * sizeof(float), conc + (size_t)off * c.G + off,
+                        (size_t)c.G * sizeof(float), n * sizeof(float), n, hipMemcpyDeviceToHost));
+    HIP_TRY(hipMemcpy(K.data(), h->K, K.size() * sizeof(float), hipMemcpyDeviceToHost));
+    int counters[3] = {0, 0, 0}, capacity = 0;
+    if (pool) {
+        PoolArgs pa;
+        if (int rc = pool_args(pool, &pa)) return rc;
+        HIP_TRY(hipMemcpy(counters, pool->counters, sizeof counters, hipMemcpyDeviceToHost));
+        capacity = pool->capacity;
+    }
+    std::string r;
+    char tmp[96];
+    auto put = [&](const char* fmt, auto... v) {
+        snprintf(tmp, sizeof tmp, fmt, v...);
+        r += tmp;
+    };
+    put("{\"gen\":%d,\"elapsed\":%.2f,", generation, elapsed);
+    r += "\"chemical\":{\"concentration\":[";
+    for (size_t i = 0; i < sample.size(); ++i) put(i ? ",%.4f" : "%.4f", (double)sample[i]);
+    put("],\"size\":%d},", n);
+    r += "\"ca\":{\"flow_kernels\":[";
+    for (int hh = 0; hh < c.H; ++hh) {
+        r += hh ? ",[" : "[";
+        for (int k = 0; k < 9; ++k) put(k ? ",%.4f" : "%.4f", (double)K[(size_t)hh * 9 + k]);
+        r += "]";
+    }
+    r += "]},\"agents\":[],\"voronoi\":[],\"archive\":{\"size\":0,\"elites\":[]},";
+    put("\"pool\":{\"active\":%d,\"capacity\":%d,", counters[0], capacity);
+    put("\"spawned\":%d,\"culled\":%d}}", counters[1], counters[2]);
+    *written = r.size();
+    if (!buf || cap < r.size() + 1)
+        return fail(SLIME_EINVAL, "snapshot needs %zu bytes, buffer has %zu", r.size() + 1, buf ? cap : 0);
+    std::memcpy(buf, r.c_str(), r.size() + 1);
+    return SLIME_OK;
+}
+
 int slime_ca_uses_mfma(const slime_ca* h) {
     if (!h) return 0;
     const slime_ca_config& c = h->cfg;

@@ -16,7 +16,7 @@ def _header_functions():
     with open(os.path.join(ROOT, "include", "slime_ca.h")) as f:
         text = f.read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(slime_(?:ca|neural_ca|pool)_\w+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(slime_(?:ca|neural_ca|pool|snapshot)_\w+)\s*\(", text)))
 
 
 def test_header_declares_the_exported_set():
