@@ -20,8 +20,9 @@
 // Scatters run as gathers: cell q collects from the cells r = q - offset_k whose
 // neighbour k it is, so no atomics are needed and every sum has a fixed order.
 //
-// Work split: one lane per (cell, head, channel) with the D lanes of a (cell,
-// head) adjacent; the per-(cell, head) dot products reduce over those D lanes.
+// Work split: one lane per 4 channels of a (cell, head) (8- or 16-byte loads), the
+// D/4 lanes of a (cell, head) adjacent; the per-(cell, head) dot products reduce
+// over those lanes with DPP moves inside a 16-lane row.
 // Parameter partial sums are kept per workgroup, each workgroup owning one
 // (pod, head), and added in a fixed order by the finalize kernels.
 #include "common.hpp"
@@ -35,15 +36,6 @@ __device__ __forceinline__ int wrapb(int v, int G) { return v < 0 ? v + G : (v >
 template <typename T>
 __device__ __forceinline__ float ld(const void* p, long long i) {
     return Store<T>::to_f32(static_cast<const T*>(p)[i]);
-}
-
-// Sum over groups of kD adjacent lanes (kD = 8 .. 64), every lane of the group
-// receiving the sum.
-template <int kD>
-__device__ __forceinline__ float dsum(float v) {
-#pragma unroll
-    for (int m = kD / 2; m > 0; m >>= 1) v += __shfl_xor(v, m, 64);
-    return v;
 }
 
 __device__ __forceinline__ float gelu_grad(float x) {
@@ -125,20 +117,73 @@ __global__ __launch_bounds__(64) void bw_loss_finalize_kernel(BackwardArgs a) {
 }
 
 // ---- per (cell, head): S7, S6, S3, S5, S4 backward and the tape for the gathers ------------
-// Block (pod, head, w): the lanes of group g handle cells i = w*gpw + g (+ stride)
-// of the pod's batches for that head. Per-thread parameter partials (M column h,
-// K row h, mu, sigma) are reduced over the block and written once.
+// Block (pod, head, w): each group of kL = D/4 lanes owns one (cell, head), a lane 4
+// consecutive channels (8- or 16-byte loads), and the per-(cell, head) dot products
+// reduce over the group with DPP lane moves. Group g handles cells i = w*groups + g
+// (+ stride) of the pod's batches. Per-thread parameter partials (M column h, K row
+// h, mu, sigma) are reduced over the block and written once.
 constexpr int kPartF = kHeads + 9 + 2;  // gM[o][h] (8), gK[h][k] (9), gmu, gsigma
+
+struct F4 {
+    float v[4];
+};
+
+template <typename T>
+__device__ __forceinline__ F4 ld4(const void* p, long long i) {  // i: a multiple of 4
+    F4 r;
+    if constexpr (sizeof(T) == 2) {
+        const uint2 w = *reinterpret_cast<const uint2*>(static_cast<const T*>(p) + i);
+        r.v[0] = bf16lo(w.x);
+        r.v[1] = bf16hi(w.x);
+        r.v[2] = bf16lo(w.y);
+        r.v[3] = bf16hi(w.y);
+    } else {
+        const float4 f = *reinterpret_cast<const float4*>(static_cast<const float*>(p) + i);
+        r.v[0] = f.x;
+        r.v[1] = f.y;
+        r.v[2] = f.z;
+        r.v[3] = f.w;
+    }
+    return r;
+}
+__device__ __forceinline__ F4 ld4f(const float* p, long long i) {
+    const float4 f = *reinterpret_cast<const float4*>(p + i);
+    return F4{{f.x, f.y, f.z, f.w}};
+}
+__device__ __forceinline__ void st4f(float* p, long long i, const float (&v)[4]) {
+    *reinterpret_cast<float4*>(p + i) = make_float4(v[0], v[1], v[2], v[3]);
+}
+template <typename T>
+__device__ __forceinline__ void st4(void* p, long long i, const float (&v)[4]) {
+    if constexpr (sizeof(T) == 2)
+        *reinterpret_cast<uint2*>(static_cast<T*>(p) + i) =
+            make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+    else
+        *reinterpret_cast<float4*>(static_cast<float*>(p) + i) = make_float4(v[0], v[1], v[2], v[3]);
+}
+
+// Sum over groups of kL adjacent lanes (kL = 2 .. 16, inside one 16-lane DPP row),
+// every lane of the group receiving the sum.
+template <int kL>
+__device__ __forceinline__ float lanes_sum(float v) {
+    if constexpr (kL >= 2) v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
+    if constexpr (kL >= 4) v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]
+    if constexpr (kL >= 8) v += dpp_f32<0x141>(v);  // row_half_mirror
+    if constexpr (kL >= 16) v += dpp_f32<0x140>(v); // row_mirror
+    return v;
+}
 
 template <typename T, int kD>
 __global__ __launch_bounds__(256) void bw_cell_kernel(BackwardArgs a) {
-    constexpr int H = kHeads, C = H * kD, kGroups = 256 / kD;
+    constexpr int H = kHeads, C = H * kD, kL = kD / 4, kGroups = 256 / kL;
+    static_assert(kL >= 2 && kL <= 16, "4 channels per lane, groups inside a DPP row");
     const int G = a.G;
     const long long cells = (long long)G * G;
     const int w = blockIdx.x % a.nW;
     const int h = (blockIdx.x / a.nW) % H;
     const int pod = blockIdx.x / (a.nW * H);
-    const int grp = threadIdx.x / kD, c = threadIdx.x % kD;
+    const int grp = threadIdx.x / kL, li = threadIdx.x % kL;
+    const int c0 = 4 * li;
     const long long pod_cells = (long long)a.per_pod * cells;
     const float inv_sqrt_d = 1.0f / __builtin_sqrtf((float)kD);
     const float dt = a.dt;
@@ -159,29 +204,21 @@ __global__ __launch_bounds__(256) void bw_cell_kernel(BackwardArgs a) {
         const long long cell = i % cells;
         const int y = (int)(cell / G), x = (int)(cell % G);
         const long long r = (long long)b * cells + cell;
-        const long long ir = r * C + h * kD + c;
-        // S7 -> gY for every output head o at (r, c); S6 -> gZ_h
-        float gz = 0.f;
-        float gy[H];
-#pragma unroll
-        for (int o = 0; o < H; ++o) {
-            const long long io = r * C + o * kD + c;
-            const float rs = a.scale[b * H + o];
-            const float e = rs * a.Y[io] - ld<T>(a.T, io);
-            const float gyp = 2.0f * e * a.inv_n;
-            gy[o] = a.coef[(b * H + o) * 2] * (gyp - a.coef[(b * H + o) * 2 + 1]);
-            gz = __builtin_fmaf(mcol[o], gy[o], gz);
-        }
-        // forward locals of head h at r
+        const long long ir = r * C + h * kD + c0;
         long long nb[9];
-        float u = 0.f;
+#pragma unroll
+        for (int k = 0; k < 9; ++k)
+            nb[k] = ((long long)b * cells + (long long)wrapb(y + k / 3 - 1, G) * G + wrapb(x + k % 3 - 1, G)) * C +
+                    h * kD + c0;
+        // ---- forward locals of head h at r (4 channels) ----
+        F4 xk[9], ik[9], vk[9];
 #pragma unroll
         for (int k = 0; k < 9; ++k) {
-            const long long q = (long long)b * cells + (long long)wrapb(y + k / 3 - 1, G) * G +
-                                wrapb(x + k % 3 - 1, G);
-            nb[k] = q * C + h * kD + c;
-            u = __builtin_fmaf(kw[k], ld<T>(a.X, nb[k]), u);
+            xk[k] = ld4<T>(a.X, nb[k]);
+            ik[k] = ld4<T>(a.I, nb[k]);
+            vk[k] = ld4<T>(a.V, nb[k]);
         }
+        const F4 pc = ld4<T>(a.P, ir);
         float mu, sg;
         if (a.per_cell) {
             const long long pi = ((long long)pod * cells + cell) * H + h;
@@ -192,14 +229,23 @@ __global__ __launch_bounds__(256) void bw_cell_kernel(BackwardArgs a) {
             sg = a.sigma[pod * H + h];
         }
         const float sp = sg + 1e-7f;
-        const float t = (u - mu) / sp;
-        const float et = __expf(-t * t);
-        const float g = 2.0f * et - 1.0f;
-        const float pc = ld<T>(a.P, ir);
+        float t[4], et[4], g[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float u = 0.f;
+#pragma unroll
+            for (int k = 0; k < 9; ++k) u = __builtin_fmaf(kw[k], xk[k].v[e], u);
+            t[e] = (u - mu) / sp;
+            et[e] = __expf(-t[e] * t[e]);
+            g[e] = 2.0f * et[e] - 1.0f;
+        }
         float s[9], mx = -3.0e38f;
 #pragma unroll
         for (int k = 0; k < 9; ++k) {
-            s[k] = dsum<kD>(pc * ld<T>(a.I, nb[k])) * inv_sqrt_d;
+            float d = 0.f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) d = __builtin_fmaf(pc.v[e], ik[k].v[e], d);
+            s[k] = lanes_sum<kL>(d) * inv_sqrt_d;
             mx = fmaxf(mx, s[k]);
         }
         float den = 0.f;
@@ -208,55 +254,88 @@ __global__ __launch_bounds__(256) void bw_cell_kernel(BackwardArgs a) {
             s[k] = __expf(s[k] - mx);
             den += s[k];
         }
-        float vt = 0.f, vn[9];
+        float vt[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int k = 0; k < 9; ++k) {
             s[k] /= den;  // a_k
-            vn[k] = ld<T>(a.V, nb[k]);
-            vt = __builtin_fmaf(s[k], vn[k], vt);
-        }
-        const float xr = ld<T>(a.X, ir);
-        const float z = __builtin_fmaf(dt * g, vt, xr);
 #pragma unroll
-        for (int o = 0; o < H; ++o) pM[o] = __builtin_fmaf(gy[o], z, pM[o]);
-        // S6, S3
-        const float gg = dt * gz * vt, gvt = dt * gz * g;
-        const float gu = gg * (-4.0f * t * et) / sp;
+            for (int e = 0; e < 4; ++e) vt[e] = __builtin_fmaf(s[k], vk[k].v[e], vt[e]);
+        }
+        float z[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) z[e] = __builtin_fmaf(dt * g[e], vt[e], xk[4].v[e]);
+        // ---- S7 -> gY for every output head o at (r, c0..c0+3); S6 -> gZ_h ----
+        float gz[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int o = 0; o < H; ++o) {
+            const long long io = r * C + o * kD + c0;
+            const float rs = a.scale[b * H + o];
+            const float cy = a.coef[(b * H + o) * 2], cq = a.coef[(b * H + o) * 2 + 1];
+            const F4 yv = ld4f(a.Y, io), tv = ld4<T>(a.T, io);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float gy = cy * (2.0f * (rs * yv.v[e] - tv.v[e]) * a.inv_n - cq);
+                gz[e] = __builtin_fmaf(mcol[o], gy, gz[e]);
+                pM[o] = __builtin_fmaf(gy, z[e], pM[o]);
+            }
+        }
+        // ---- S6, S3 ----
+        float gu[4], gvt[4], gmu_l = 0.f, gsg_l = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float gg = dt * gz[e] * vt[e];
+            gvt[e] = dt * gz[e] * g[e];
+            gu[e] = gg * (-4.0f * t[e] * et[e]) / sp;
+            gmu_l -= gu[e];
+            gsg_l -= gu[e] * t[e];
+        }
         if (a.per_cell) {
-            const float smu = dsum<kD>(-gu), ssg = dsum<kD>(-gu * t);
-            if (c == 0) {
+            const float smu = lanes_sum<kL>(gmu_l), ssg = lanes_sum<kL>(gsg_l);
+            if (li == 0) {
                 a.gcell[(r * H + h) * 2 + 0] = smu;
                 a.gcell[(r * H + h) * 2 + 1] = ssg;
             }
         } else {
-            pmu -= gu;
-            psg -= gu * t;
+            pmu += gmu_l;
+            psg += gsg_l;
         }
 #pragma unroll
-        for (int k = 0; k < 9; ++k) pK[k] = __builtin_fmaf(gu, ld<T>(a.X, nb[k]), pK[k]);
-        // S5, S4
+        for (int k = 0; k < 9; ++k)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) pK[k] = __builtin_fmaf(gu[e], xk[k].v[e], pK[k]);
+        // ---- S5, S4 ----
         float ga[9], sa = 0.f;
 #pragma unroll
         for (int k = 0; k < 9; ++k) {
-            ga[k] = dsum<kD>(gvt * vn[k]);
+            float d = 0.f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) d = __builtin_fmaf(gvt[e], vk[k].v[e], d);
+            ga[k] = lanes_sum<kL>(d);
             sa = __builtin_fmaf(s[k], ga[k], sa);
         }
-        float gp = 0.f;
+        float gp[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int k = 0; k < 9; ++k) {
             const float gs = s[k] * (ga[k] - sa);
-            gp = __builtin_fmaf(gs * inv_sqrt_d, ld<T>(a.I, nb[k]), gp);
-            if (k % kD == c) {  // the tape for the gathers: a_k and gs_k per (r, h)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) gp[e] = __builtin_fmaf(gs * inv_sqrt_d, ik[k].v[e], gp[e]);
+            if (k % kL == li) {  // the tape for the gathers: a_k and gs_k per (r, h)
                 a.att[(r * H + h) * 9 + k] = s[k];
                 a.gS[(r * H + h) * 9 + k] = gs;
             }
         }
-        a.gU[ir] = gu;
-        a.gVt[ir] = gvt;
+        st4f(a.gU, ir, gu);
+        st4f(a.gVt, ir, gvt);
         // gP~ -> plane 0 of G3; the direct part of gX
-        const float gpt = pc > 0.f ? gp : 0.f;
-        static_cast<T*>(a.G3)[r * 3 * C + h * kD + c] = Store<T>::from_f32(gpt);
-        a.gXd[ir] = gz + a.coef[(b * H + h) * 2 + 1];
+        float gpt[4], gxd[4];
+        const float cqh = a.coef[(b * H + h) * 2 + 1];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            gpt[e] = pc.v[e] > 0.f ? gp[e] : 0.f;
+            gxd[e] = gz[e] + cqh;
+        }
+        st4<T>(a.G3, r * 3 * C + h * kD + c0, gpt);
+        st4f(a.gXd, ir, gxd);
     }
     // block reduction of the parameter partials, fixed order
     __shared__ float red[kPartF][256];
@@ -277,13 +356,16 @@ __global__ __launch_bounds__(256) void bw_cell_kernel(BackwardArgs a) {
 }
 
 // ---- gathers: gV, gI~ (planes 2 and 1 of G3) and the potential's transpose -------------------
+// One lane per 4 channels of one (cell q, head): cell q collects from the 9 cells
+// r = q - offset_k whose neighbour k it is.
 template <typename T, int kD>
 __global__ __launch_bounds__(256) void bw_gather_kernel(BackwardArgs a) {
     constexpr int H = kHeads, C = H * kD;
     const int G = a.G;
     const long long cells = (long long)G * G;
-    const long long e = (long long)blockIdx.x * 256 + threadIdx.x;
-    if (e >= (long long)a.B * cells * C) return;
+    const long long e4 = (long long)blockIdx.x * 256 + threadIdx.x;  // 4-channel unit
+    if (e4 * 4 >= (long long)a.B * cells * C) return;
+    const long long e = e4 * 4;
     const long long q = e / C;
     const int ch = (int)(e % C), h = ch / kD;
     const int b = (int)(q / cells);
@@ -291,22 +373,33 @@ __global__ __launch_bounds__(256) void bw_gather_kernel(BackwardArgs a) {
     const int y = (int)(cell / G), x = (int)(cell % G);
     const int pod = b / a.per_pod;
     const float inv_sqrt_d = 1.0f / __builtin_sqrtf((float)kD);
-    float gv = 0.f, gi = 0.f, gx = 0.f;
+    float gv[4] = {0.f, 0.f, 0.f, 0.f}, gi[4] = {0.f, 0.f, 0.f, 0.f}, gx[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int k = 0; k < 9; ++k) {
-        // r = q - offset_k: the cell whose neighbour k is q
         const long long r = (long long)b * cells + (long long)wrapb(y - (k / 3 - 1), G) * G +
                             wrapb(x - (k % 3 - 1), G);
         const long long ir = r * C + ch;
-        const float ak = a.att[(r * H + h) * 9 + k], gs = a.gS[(r * H + h) * 9 + k];
-        gv = __builtin_fmaf(ak, a.gVt[ir], gv);
-        gi = __builtin_fmaf(gs * inv_sqrt_d, ld<T>(a.P, ir), gi);
-        gx = __builtin_fmaf(a.K[(pod * H + h) * 9 + k], a.gU[ir], gx);
+        const float ak = a.att[(r * H + h) * 9 + k], gs = a.gS[(r * H + h) * 9 + k] * inv_sqrt_d;
+        const float kk = a.K[(pod * H + h) * 9 + k];
+        const F4 gvt = ld4f(a.gVt, ir), pr = ld4<T>(a.P, ir), gu = ld4f(a.gU, ir);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            gv[j] = __builtin_fmaf(ak, gvt.v[j], gv[j]);
+            gi[j] = __builtin_fmaf(gs, pr.v[j], gi[j]);
+            gx[j] = __builtin_fmaf(kk, gu.v[j], gx[j]);
+        }
     }
-    T* g3 = static_cast<T*>(a.G3) + q * 3 * C;
-    g3[C + ch] = Store<T>::from_f32(gi * gelu_grad(ld<T>(a.Ipre, e)));
-    g3[2 * C + ch] = Store<T>::from_f32(gv);
-    a.gXd[e] += gx;
+    const F4 ip = ld4<T>(a.Ipre, e);
+    const F4 gd = ld4f(a.gXd, e);
+    float g1[4], gxd[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        g1[j] = gi[j] * gelu_grad(ip.v[j]);
+        gxd[j] = gd.v[j] + gx[j];
+    }
+    st4<T>(a.G3, q * 3 * C + C + ch, g1);
+    st4<T>(a.G3, q * 3 * C + 2 * C + ch, gv);
+    st4f(a.gXd, e, gxd);
 }
 
 // ---- parameter finalize: fixed-order sums of the per-block partials ----------------------------
@@ -414,7 +507,7 @@ hipError_t launch_dt(const BackwardArgs& a, hipStream_t s) {
     hipLaunchKernelGGL((bw_loss_partial_kernel<T>), dim3(a.lchunks, a.B), dim3(256), 0, s, a);
     hipLaunchKernelGGL(bw_loss_finalize_kernel, dim3((a.B * kHeads + 63) / 64), dim3(64), 0, s, a);
     hipLaunchKernelGGL((bw_cell_kernel<T, kD>), dim3(a.pods * kHeads * a.nW), dim3(256), 0, s, a);
-    hipLaunchKernelGGL((bw_gather_kernel<T, kD>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((bw_gather_kernel<T, kD>), dim3((unsigned)((n / 4 + 255) / 256)), dim3(256), 0, s, a);
     hipLaunchKernelGGL(bw_param_finalize_kernel, dim3((a.pods * kHeads * kPartF + 63) / 64), dim3(64), 0,
                        s, a);
     if (a.per_cell)
