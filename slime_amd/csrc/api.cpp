@@ -618,7 +618,7 @@ int slime_ca_backward(slime_ca* h, const void* x_in, const void* target, float* 
     const int lchunks = backward_loss_chunks(c.G);
     const int nW = 128;
     const long long rows_pod = (long long)(c.B / c.pods) * c.G * c.G;
-    const int dw_chunks = backward_dw_chunks_per_pod(rows_pod);
+    const int dw_chunks = backward_dw_chunks_per_pod(c.dtype, (int)C, rows_pod);
     const bool want_w = grads && (grads->WP || grads->WI || grads->WV);
     // work buffers, allocated on first use
     if (!h->Wcat) {
@@ -746,6 +746,7 @@ int slime_ca_backward(slime_ca* h, const void* x_in, const void* target, float* 
         d.pods = c.pods;
         d.chunks_per_pod = dw_chunks;
         d.rows_per_pod = rows_pod;
+        d.rows_per_chunk = backward_dw_rows_per_chunk(c.dtype, (int)C, rows_pod);
         d.gWP = grads->WP;
         d.gWI = grads->WI;
         d.gWV = grads->WV;

@@ -38,92 +38,6 @@ __device__ __forceinline__ float ld(const void* p, long long i) {
     return Store<T>::to_f32(static_cast<const T*>(p)[i]);
 }
 
-__device__ __forceinline__ float gelu_grad(float x) {
-    const float c0 = 0.7978845608028654f, c1 = 0.044715f;
-    const float th = tanhf(c0 * (x + c1 * x * x * x));
-    return 0.5f * (1.0f + th) + 0.5f * x * (1.0f - th * th) * c0 * (1.0f + 3.0f * c1 * x * x);
-}
-
-// ---- S7: loss, Q_o, B_o partial sums ---------------------------------------------------
-// Block (b, chunk) covers kLossCells cells of batch b; thread t owns channels t,
-// t + 256, ... and accumulates per head in fp64.
-constexpr int kLossCells = 64;
-
-template <typename T>
-__global__ __launch_bounds__(256) void bw_loss_partial_kernel(BackwardArgs a) {
-    const int b = blockIdx.y, chunk = blockIdx.x;
-    const int C = kHeads * a.D;
-    const long long cells = (long long)a.G * a.G;
-    const double N = (double)a.B * (double)cells * C;
-    __shared__ double s[3][kHeads][256];
-    double acc[3][kHeads];
-#pragma unroll
-    for (int q = 0; q < 3; ++q)
-#pragma unroll
-        for (int h = 0; h < kHeads; ++h) acc[q][h] = 0.0;
-    for (int c0 = 0; c0 < kLossCells; ++c0) {
-        const long long cell = (long long)chunk * kLossCells + c0;
-        if (cell >= cells) break;
-        const long long base = ((long long)b * cells + cell) * C;
-        for (int ch = threadIdx.x; ch < C; ch += 256) {
-            const int h = ch / a.D;
-            const float r = a.scale[b * kHeads + h];
-            const double y = a.Y[base + ch];
-            const double e = (double)r * y - (double)ld<T>(a.T, base + ch);
-#pragma unroll
-            for (int hh = 0; hh < kHeads; ++hh)
-                if (hh == h) {
-                    acc[0][hh] += e * e;
-                    acc[1][hh] += 2.0 * e / N * y;
-                    acc[2][hh] += y;
-                }
-        }
-    }
-#pragma unroll
-    for (int q = 0; q < 3; ++q)
-#pragma unroll
-        for (int h = 0; h < kHeads; ++h) s[q][h][threadIdx.x] = acc[q][h];
-    __syncthreads();
-    for (int w = 128; w > 0; w >>= 1) {
-        if ((int)threadIdx.x < w)
-#pragma unroll
-            for (int q = 0; q < 3; ++q)
-#pragma unroll
-                for (int h = 0; h < kHeads; ++h) s[q][h][threadIdx.x] += s[q][h][threadIdx.x + w];
-        __syncthreads();
-    }
-    if (threadIdx.x < 3 * kHeads) {
-        const int q = threadIdx.x / kHeads, h = threadIdx.x % kHeads;
-        a.lpart[(((long long)b * kHeads + h) * a.lchunks + chunk) * 3 + q] = s[q][h][0];
-    }
-}
-
-// One thread per (b, head): fixed-order sums of the partials, then the S7 chain
-// coefficients: gY = cY (gY' - cQ), and cQ is also the uniform direct term of gX.
-__global__ __launch_bounds__(64) void bw_loss_finalize_kernel(BackwardArgs a) {
-    const int bh = blockIdx.x * 64 + threadIdx.x;
-    if (bh >= a.B * kHeads) return;
-    double l = 0.0, q = 0.0, bs = 0.0;
-    for (int c = 0; c < a.lchunks; ++c) {
-        const double* p = a.lpart + ((long long)bh * a.lchunks + c) * 3;
-        l += p[0];
-        q += p[1];
-        bs += p[2];
-    }
-    const bool guard = fabs(bs) > 1e-6;
-    a.coef[bh * 2 + 0] = guard ? a.scale[bh] : 1.0f;
-    a.coef[bh * 2 + 1] = guard ? (float)(q / bs) : 0.0f;
-    a.loss_bh[bh] = l;
-}
-
-// ---- per (cell, head): S7, S6, S3, S5, S4 backward and the tape for the gathers ------------
-// Block (pod, head, w): each group of kL = D/4 lanes owns one (cell, head), a lane 4
-// consecutive channels (8- or 16-byte loads), and the per-(cell, head) dot products
-// reduce over the group with DPP lane moves. Group g handles cells i = w*groups + g
-// (+ stride) of the pod's batches. Per-thread parameter partials (M column h, K row
-// h, mu, sigma) are reduced over the block and written once.
-constexpr int kPartF = kHeads + 9 + 2;  // gM[o][h] (8), gK[h][k] (9), gmu, gsigma
-
 struct F4 {
     float v[4];
 };
@@ -161,6 +75,101 @@ __device__ __forceinline__ void st4(void* p, long long i, const float (&v)[4]) {
     else
         *reinterpret_cast<float4*>(static_cast<float*>(p) + i) = make_float4(v[0], v[1], v[2], v[3]);
 }
+
+__device__ __forceinline__ float gelu_grad(float x) {
+    const float c0 = 0.7978845608028654f, c1 = 0.044715f;
+    const float th = tanhf(c0 * (x + c1 * x * x * x));
+    return 0.5f * (1.0f + th) + 0.5f * x * (1.0f - th * th) * c0 * (1.0f + 3.0f * c1 * x * x);
+}
+
+// ---- S7: loss, Q_o, B_o partial sums ---------------------------------------------------
+// Block (chunk, b) covers kLossCells cells of batch b; lane t of a cell slot owns
+// channels 4t .. 4t+3 (one head) and accumulates in fp64; the block then adds the
+// lanes of each head in a fixed tree order.
+constexpr int kLossCells = 64;
+
+template <typename T>
+__global__ __launch_bounds__(256) void bw_loss_partial_kernel(BackwardArgs a) {
+    const int b = blockIdx.y, chunk = blockIdx.x;
+    const int C = kHeads * a.D, lanes = C / 4;      // lanes per cell
+    const int slots = 256 / lanes;                  // cells per pass (C <= 1024)
+    const int slot = threadIdx.x / lanes, t = threadIdx.x % lanes;
+    const int h = 4 * t / a.D;
+    const long long cells = (long long)a.G * a.G;
+    const double N = (double)a.B * (double)cells * C;
+    const float r = a.scale[b * kHeads + h];
+    double l = 0.0, q = 0.0, bs = 0.0;
+    if (slot < slots) {
+        for (int c0 = slot; c0 < kLossCells; c0 += slots) {
+            const long long cell = (long long)chunk * kLossCells + c0;
+            if (cell >= cells) break;
+            const long long base = ((long long)b * cells + cell) * C + 4 * t;
+            const F4 y = ld4f(a.Y, base), tv = ld4<T>(a.T, base);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const double yd = y.v[e];
+                const double err = (double)r * yd - (double)tv.v[e];
+                l += err * err;
+                q += err * yd;
+                bs += yd;
+            }
+        }
+    }
+    // per-head sums over the block: lanes of head h are (slot, t) with 4t / D == h
+    __shared__ double s[3][256];
+    s[0][threadIdx.x] = l;
+    s[1][threadIdx.x] = q * (2.0 / N);
+    s[2][threadIdx.x] = bs;
+    __syncthreads();
+    if (threadIdx.x < 3 * kHeads) {
+        const int qq = threadIdx.x / kHeads, hh = threadIdx.x % kHeads;
+        const int per_head = a.D / 4;  // lanes of one head in one slot
+        double sum = 0.0;
+        for (int sl = 0; sl < slots; ++sl)
+            for (int u = 0; u < per_head; ++u) sum += s[qq][sl * lanes + hh * per_head + u];
+        a.lpart[(((long long)b * kHeads + hh) * a.lchunks + chunk) * 3 + qq] = sum;
+    }
+}
+
+// One block per (b, head): fixed-order sums of the partials (strided per lane, then
+// a tree), then the S7 chain coefficients: gY = cY (gY' - cQ), and cQ is also the
+// uniform direct term of gX.
+__global__ __launch_bounds__(256) void bw_loss_finalize_kernel(BackwardArgs a) {
+    const int bh = blockIdx.x;
+    __shared__ double s[3][256];
+    double l = 0.0, q = 0.0, bs = 0.0;
+    for (int c = threadIdx.x; c < a.lchunks; c += 256) {
+        const double* p = a.lpart + ((long long)bh * a.lchunks + c) * 3;
+        l += p[0];
+        q += p[1];
+        bs += p[2];
+    }
+    s[0][threadIdx.x] = l;
+    s[1][threadIdx.x] = q;
+    s[2][threadIdx.x] = bs;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w)
+#pragma unroll
+            for (int k = 0; k < 3; ++k) s[k][threadIdx.x] += s[k][threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        const double ls = s[0][0], qs = s[1][0], b_s = s[2][0];
+        const bool guard = fabs(b_s) > 1e-6;
+        a.coef[bh * 2 + 0] = guard ? a.scale[bh] : 1.0f;
+        a.coef[bh * 2 + 1] = guard ? (float)(qs / b_s) : 0.0f;
+        a.loss_bh[bh] = ls;
+    }
+}
+
+// ---- per (cell, head): S7, S6, S3, S5, S4 backward and the tape for the gathers ------------
+// Block (pod, head, w): each group of kL = D/4 lanes owns one (cell, head), a lane 4
+// consecutive channels (8- or 16-byte loads), and the per-(cell, head) dot products
+// reduce over the group with DPP lane moves. Group g handles cells i = w*groups + g
+// (+ stride) of the pod's batches. Per-thread parameter partials (M column h, K row
+// h, mu, sigma) are reduced over the block and written once.
+constexpr int kPartF = kHeads + 9 + 2;  // gM[o][h] (8), gK[h][k] (9), gmu, gsigma
 
 // Sum over groups of kL adjacent lanes (kL = 2 .. 16, inside one 16-lane DPP row),
 // every lane of the group receiving the sum.
@@ -450,8 +459,8 @@ __global__ __launch_bounds__(256) void bw_dw_partial_kernel(BackwardArgs a, DwAr
     const int kt = blockIdx.x, jt = blockIdx.y, chunk = blockIdx.z;
     const long long rows = d.rows_per_pod;
     const int pod = chunk / d.chunks_per_pod;
-    const long long r0 = (long long)pod * rows + (long long)(chunk % d.chunks_per_pod) * kWRows;
-    const long long r1 = min(r0 + kWRows, (long long)(pod + 1) * rows);
+    const long long r0 = (long long)pod * rows + (long long)(chunk % d.chunks_per_pod) * d.rows_per_chunk;
+    const long long r1 = min(r0 + d.rows_per_chunk, (long long)(pod + 1) * rows);
     __shared__ float sx[16][64], sg[16][64];
     const int tk = (threadIdx.x / 16) * 4, tj = (threadIdx.x % 16) * 4;
     float acc[4][4] = {};
@@ -476,6 +485,140 @@ __global__ __launch_bounds__(256) void bw_dw_partial_kernel(BackwardArgs a, DwAr
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) out[(long long)(kt * 64 + tk + i) * N3 + jt * 64 + tj + j] = acc[i][j];
+}
+
+// bf16: the same partial sums on the matrix cores. Block (k tile, j tile, chunk):
+// a 128 x 128 output tile over rows_per_chunk rows in steps of 32, wave (wk, wj)
+// owning 64 x 64 as 4 x 4 v_mfma_f32_16x16x32_bf16 blocks. Both operands are
+// column slices of row-major tiles -- out[k][j] = sum_r X[r][k] G[r][j] -- staged
+// as [32 rows][128 columns] (256-byte rows) by direct global->LDS loads through a
+// 4-stage ring (three steps in flight), and read with ds_read_b64_tr_b16: in a
+// 16-lane group, lane j reads 4 columns of row rbase + j / 4, and lane i then holds
+// column i of rows rbase .. rbase + 3, the MFMA operand layout (8 consecutive rows
+// of one column per lane, two reads). The 16-byte chunks of row r sit at chunk ^
+// 2 (r % 4), so the four rows of a read fall in disjoint banks.
+constexpr int kDwT = 128, kDwStep = 32, kDwRowB = 2 * kDwT, kDwStages = 4;
+constexpr int kDwStageB = 2 * kDwStep * kDwRowB;  // X and G tiles, 16 KiB
+constexpr long long kDwRowsMfma = 16384;
+
+typedef short dw_v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) dw_v4i16 dw_lds_v4i16;
+typedef __attribute__((address_space(3))) void dw_lds_void;
+
+__device__ __forceinline__ uint2 dw_tr16(const unsigned char* p) {
+    const dw_v4i16 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (dw_lds_v4i16*)(const __attribute__((address_space(3))) unsigned char*)(p));
+    return __builtin_bit_cast(uint2, v);
+}
+
+// One direct global->LDS load (global_load_lds_dwordx4, SGPR base + 32-bit lane
+// offset): lane l's 16 bytes land at LDS byte address lds + 16 l. The ring waits
+// for these loads itself (dw_wait) before the barrier that publishes a stage.
+__device__ __forceinline__ void dw_dma16(const void* base, unsigned voff, unsigned lds) {
+    asm volatile(
+        "s_mov_b32 m0, %0\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, %2"
+        :
+        : "s"(lds), "v"(voff), "s"(base)
+        : "memory", "m0");
+}
+template <int N>
+__device__ __forceinline__ void dw_wait() {
+    __builtin_amdgcn_s_waitcnt((N & 15) | (((N >> 4) & 3) << 14) | 0x0F70);
+}
+__device__ __forceinline__ void dw_barrier() {  // LDS data only (no vmcnt drain)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // s_waitcnt lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+__global__ __launch_bounds__(256) void bw_dw_mfma_kernel(BackwardArgs a, DwArgs d) {
+    __shared__ __attribute__((aligned(1024))) unsigned char lds[kDwStages * kDwStageB];
+    const int C = d.C, N3 = 3 * C;
+    const int kt = blockIdx.x, jt = blockIdx.y, chunk = blockIdx.z;
+    const int pod = chunk / d.chunks_per_pod;
+    const long long r0 = (long long)pod * d.rows_per_pod + (long long)(chunk % d.chunks_per_pod) * d.rows_per_chunk;
+    const long long r1 = min(r0 + d.rows_per_chunk, (long long)(pod + 1) * d.rows_per_pod);
+    const int nsteps = (int)((r1 - r0) / kDwStep);  // rows are a multiple of kDwStep (host-checked)
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wk = wave & 1, wj = wave >> 1;
+    const char* Xs = reinterpret_cast<const char*>(static_cast<const bf16_t*>(a.X) + r0 * C + (long long)kt * kDwT);
+    const char* Gs = reinterpret_cast<const char*>(static_cast<const bf16_t*>(a.G3) + r0 * N3 + (long long)jt * kDwT);
+    // Direct loads: instruction q of a tile fills rows 4 q .. 4 q + 3; lane l lands in
+    // row l / 16 of those, physical chunk l % 16, fetching logical chunk
+    // (l % 16) ^ 2 (l / 16). Wave w issues instructions 2 w and 2 w + 1 of each tile.
+    const int drow = lane >> 4, dchunk = (lane & 15) ^ (2 * drow);
+    const unsigned xoff = (unsigned)(drow * C * 2 + dchunk * 16), goff = (unsigned)(drow * N3 * 2 + dchunk * 16);
+    auto issue = [&](int st, int stage) {  // step st (clamped: past the end refetch the last)
+        const long long rb = (long long)(st < nsteps ? st : nsteps - 1) * kDwStep;
+        const unsigned sb = (unsigned)(size_t)(const dw_lds_void*)(lds + stage * kDwStageB);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int q = 2 * wave + u;
+            dw_dma16(Xs + (rb + 4 * q) * C * 2, xoff, sb + q * 1024);
+            dw_dma16(Gs + (rb + 4 * q) * N3 * 2, goff, sb + kDwStep * kDwRowB + q * 1024);
+        }
+    };
+    // operand reads: 16-lane group g covers rows 8 g .. 8 g + 7 of a step (two reads)
+    const int g = lane >> 4, i = lane & 15;
+    auto rd = [&](int col0, int hf) {  // byte offset of this lane's 8 bytes in a tile
+        const int row = 8 * g + 4 * hf + (i >> 2);
+        const int chunk_l = col0 / 8 + ((i & 3) >> 1);
+        return row * kDwRowB + ((chunk_l ^ (2 * (i >> 2))) << 4) + 8 * (i & 1);
+    };
+    int roff[2][4][2];  // [x/g][block][hf]
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+            roff[0][b][hf] = rd(wk * 64 + b * 16, hf);
+            roff[1][b][hf] = kDwStep * kDwRowB + rd(wj * 64 + b * 16, hf);
+        }
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) acc[kb][jb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (nsteps > 0) {
+#pragma unroll
+        for (int st = 0; st < kDwStages - 1; ++st) issue(st, st);
+    }
+    for (int st = 0; st < nsteps; ++st) {
+        dw_wait<4 * (kDwStages - 2)>();  // this wave's loads of step st have landed
+        dw_barrier();                    // ... and every wave's; step st-1's stage is free
+        issue(st + kDwStages - 1, (st + kDwStages - 1) % kDwStages);
+        const unsigned char* base = lds + (st % kDwStages) * kDwStageB;
+        uint4 av[4], bv[4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const uint2 x0 = dw_tr16(base + roff[0][b][0]), x1 = dw_tr16(base + roff[0][b][1]);
+            const uint2 g0 = dw_tr16(base + roff[1][b][0]), g1 = dw_tr16(base + roff[1][b][1]);
+            av[b] = make_uint4(x0.x, x0.y, x1.x, x1.y);
+            bv[b] = make_uint4(g0.x, g0.y, g1.x, g1.y);
+        }
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+            for (int jb = 0; jb < 4; ++jb)
+                acc[kb][jb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    __builtin_bit_cast(bf16x8_v, av[kb]), __builtin_bit_cast(bf16x8_v, bv[jb]), acc[kb][jb], 0, 0, 0);
+    }
+    dw_wait<0>();  // refetched steps may still be landing in LDS
+    // C layout of a 16 x 16 block: lane l holds column l % 16 of rows 4 (l / 16) + e
+    float* out = d.part + (long long)chunk * C * N3;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int k = kt * kDwT + wk * 64 + kb * 16 + 4 * g + e;
+                const int j = jt * kDwT + wj * 64 + jb * 16 + i;
+                out[(long long)k * N3 + j] = acc[kb][jb][e];
+            }
 }
 
 __global__ __launch_bounds__(256) void bw_dw_reduce_kernel(DwArgs d) {
@@ -505,7 +648,7 @@ hipError_t launch_dt(const BackwardArgs& a, hipStream_t s) {
     const long long cells = (long long)a.G * a.G;
     const long long n = (long long)a.B * cells * kHeads * kD;
     hipLaunchKernelGGL((bw_loss_partial_kernel<T>), dim3(a.lchunks, a.B), dim3(256), 0, s, a);
-    hipLaunchKernelGGL(bw_loss_finalize_kernel, dim3((a.B * kHeads + 63) / 64), dim3(64), 0, s, a);
+    hipLaunchKernelGGL(bw_loss_finalize_kernel, dim3(a.B * kHeads), dim3(256), 0, s, a);
     hipLaunchKernelGGL((bw_cell_kernel<T, kD>), dim3(a.pods * kHeads * a.nW), dim3(256), 0, s, a);
     hipLaunchKernelGGL((bw_gather_kernel<T, kD>), dim3((unsigned)((n / 4 + 255) / 256)), dim3(256), 0, s, a);
     hipLaunchKernelGGL(bw_param_finalize_kernel, dim3((a.pods * kHeads * kPartF + 63) / 64), dim3(64), 0,
@@ -531,7 +674,17 @@ hipError_t launch_t(const BackwardArgs& a, hipStream_t s) {
 
 int backward_loss_chunks(int G) { return (G * G + kLossCells - 1) / kLossCells; }
 int backward_part_floats() { return kPartF; }
-int backward_dw_chunks_per_pod(long long rows_per_pod) { return (int)((rows_per_pod + kWRows - 1) / kWRows); }
+static bool dw_mfma(int dtype, int C, long long rows_per_pod) {
+    return dtype == 1 && C % kDwT == 0 && rows_per_pod % kDwStep == 0;
+}
+long long backward_dw_rows_per_chunk(int dtype, int C, long long rows_per_pod) {
+    if (!dw_mfma(dtype, C, rows_per_pod)) return kWRows;
+    return rows_per_pod < kDwRowsMfma ? rows_per_pod : kDwRowsMfma;  // a multiple of kDwStep
+}
+int backward_dw_chunks_per_pod(int dtype, int C, long long rows_per_pod) {
+    const long long r = backward_dw_rows_per_chunk(dtype, C, rows_per_pod);
+    return (int)((rows_per_pod + r - 1) / r);
+}
 
 hipError_t launch_backward_stencil(int dtype, const BackwardArgs& a, hipStream_t s) {
     return dtype == 1 ? launch_t<bf16_t>(a, s) : launch_t<float>(a, s);
@@ -539,7 +692,10 @@ hipError_t launch_backward_stencil(int dtype, const BackwardArgs& a, hipStream_t
 
 hipError_t launch_backward_dw(int dtype, const BackwardArgs& a, const DwArgs& d, hipStream_t s) {
     const dim3 grid(d.C / 64, 3 * d.C / 64, d.pods * d.chunks_per_pod);
-    if (dtype == 1)
+    if (dw_mfma(dtype, d.C, d.rows_per_pod))
+        hipLaunchKernelGGL(bw_dw_mfma_kernel, dim3(d.C / kDwT, 3 * d.C / kDwT, d.pods * d.chunks_per_pod),
+                           dim3(256), 0, s, a, d);
+    else if (dtype == 1)
         hipLaunchKernelGGL((bw_dw_partial_kernel<bf16_t>), grid, dim3(256), 0, s, a, d);
     else
         hipLaunchKernelGGL((bw_dw_partial_kernel<float>), grid, dim3(256), 0, s, a, d);

@@ -134,13 +134,16 @@ struct DwArgs {
     float* part;             // [pods * chunks_per_pod][C][3C]
     int C, pods, chunks_per_pod;
     long long rows_per_pod;
+    long long rows_per_chunk;  // backward_dw_rows_per_chunk
     float* gWP;              // [pods][C][C] each, may be nullptr
     float* gWI;
     float* gWV;
 };
 int backward_loss_chunks(int G);
 int backward_part_floats();
-int backward_dw_chunks_per_pod(long long rows_per_pod);
+// Row chunks of the weight-gradient reduction (split over rows, added in order).
+long long backward_dw_rows_per_chunk(int dtype, int C, long long rows_per_pod);
+int backward_dw_chunks_per_pod(int dtype, int C, long long rows_per_pod);
 hipError_t launch_backward_stencil(int dtype, const BackwardArgs& a, hipStream_t s);
 hipError_t launch_backward_dw(int dtype, const BackwardArgs& a, const DwArgs& d, hipStream_t s);
 hipError_t launch_backward_final(int dtype, const float* gXd, const void* gXp, float* gX, long long n,
