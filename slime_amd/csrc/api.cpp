@@ -293,7 +293,7 @@ int run_fitness(slime_ca* h, const void* x_hist, long long t_stride, int T, floa
     if (!h->mom_part || h->fit_T < T) {
         if (h->mom_part) (void)hipFree(h->mom_part);
         h->mom_part = nullptr;
-        rc = dalloc_t(&h->mom_part, BH * chunks * (size_t)(T - 1) * 5 * 8);
+        rc = dalloc_t(&h->mom_part, BH * chunks * (size_t)T * 3 * 8);
         if (rc) return rc;
         h->fit_T = T;
     }

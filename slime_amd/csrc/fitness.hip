@@ -20,6 +20,7 @@
 // fixed order, runs the cyclic Jacobi on the fp64 matrix in LDS, and finishes
 // rank, coherence and fitness.
 #include "common.hpp"
+#include "fp64.hpp"
 #include "kernels.hpp"
 
 namespace slime {
@@ -40,32 +41,74 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
     return v;
 }
 
-// Per (batch, head, chunk of cells): the D x D Gram partial of the last state and
-// the lag-1 moments of every consecutive pair of states. Products of the fp32
-// values are exact in fp64 and accumulate in fp64, so the partials carry no
-// accumulation error that the Jacobi solve could amplify on a nearly singular Gram
-// (small eigenvalues enter the rank through their square roots).
+// Up to kTB states are read per pass over a chunk; their sums stay in registers.
+constexpr int kTB = 8;
+
+// The 16-byte pieces of state t that thread `tid` owns in the stage whose head-h
+// slice starts `stage_off` bytes into each state: piece j is (cell, channel group)
+// = divmod(tid + 256 j, D / elements-per-piece). The uniform part of the address
+// is one scalar base per state; the per-thread part is a small byte offset that
+// does not change between stages or states. Pieces past the stage hold zeros.
+template <typename T, int D, int kPPT>
+__device__ __forceinline__ void load_pieces(const FitnessArgs& f, int t, long long stage_off, int tid,
+                                            uint4 (&x)[kPPT]) {
+    constexpr int kCE = 16 / (int)sizeof(T);
+    constexpr int kCPR = D / kCE;
+    constexpr int kPieces = kCellsPerStage * kCPR;
+    constexpr int C = kHeads * D;
+    const char* base = static_cast<const char*>(f.hist) + t * f.t_stride + stage_off;
+#pragma unroll
+    for (int j = 0; j < kPPT; ++j) {
+        const int q = tid + 256 * j;
+        if (kPieces % 256 == 0 || q < kPieces) {
+            const unsigned off = (unsigned)(((q / kCPR) * C + (q % kCPR) * kCE) * (int)sizeof(T));
+            x[j] = *reinterpret_cast<const uint4*>(base + off);
+        } else {
+            x[j] = make_uint4(0u, 0u, 0u, 0u);
+        }
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ void unpack_piece(const uint4& v, float (&e)[16 / sizeof(T)]) {
+    if constexpr (sizeof(T) == 2) {
+        e[0] = bf16lo(v.x), e[1] = bf16hi(v.x), e[2] = bf16lo(v.y), e[3] = bf16hi(v.y);
+        e[4] = bf16lo(v.z), e[5] = bf16hi(v.z), e[6] = bf16lo(v.w), e[7] = bf16hi(v.w);
+    } else {
+        e[0] = __builtin_bit_cast(float, v.x), e[1] = __builtin_bit_cast(float, v.y);
+        e[2] = __builtin_bit_cast(float, v.z), e[3] = __builtin_bit_cast(float, v.w);
+    }
+}
+
+// Per (batch, head, chunk of cells): the D x D Gram partial of the last state, and
+// for every state t the sums S1 = sum x_t, S2 = sum x_t^2 and P = sum x_{t-1} x_t
+// (P of state 0 is 0), which give the lag-1 moments of each consecutive pair.
+// Products of the fp32 values are exact in fp64 and accumulate in fp64, so the
+// partials carry no accumulation error that the Jacobi solve could amplify on a
+// nearly singular Gram (small eigenvalues enter the rank through their square
+// roots). Each pass over the chunk reads states tb - 1 .. tb + kTB - 1 once, with
+// 16-byte loads, all of a stage's loads in flight together; the last pass stages
+// the last state through LDS for the Gram.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void fitness_partial_kernel(FitnessArgs f) {
     constexpr int H = kHeads;
-    constexpr int C = H * D;
-    constexpr int kCE = 16 / (int)sizeof(T);   // elements per 16-byte load
-    constexpr int kCPR = D / kCE;               // 16-byte loads per cell of one head
+    constexpr int kCE = 16 / (int)sizeof(T);   // elements per 16-byte piece
+    constexpr int kCPR = D / kCE;               // pieces per cell of one head
+    constexpr int kPieces = kCellsPerStage * kCPR;
+    constexpr int kPPT = (kPieces + 255) / 256;  // pieces per thread
     constexpr int kBS = 4;                      // Gram block edge per thread
     constexpr int kBlk = D / kBS;               // blocks per side (16 at D = 64)
     static_assert(kBlk * kBlk <= 256, "one Gram block per thread");
     __shared__ __attribute__((aligned(16))) float sx[kCellsPerStage * D];
-    __shared__ double sred[4][5];
+    __shared__ double sred[4][3 * kTB];
 
     const int bh = blockIdx.x, chunk = blockIdx.y;
     const int b = bh / H, h = bh % H;
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const long long cells = (long long)f.G * f.G;
     const long long cpc = cells / f.chunks;
     const long long c_begin = chunk * cpc;
-    const T* last = history_state<T>(f, f.T - 1);
 
-    // ---- Gram partial of the last state -----------------------------------------
     const bool gact = tid < kBlk * kBlk;
     const int bi = tid / kBlk, bj = tid % kBlk;
     double g[kBS][kBS];
@@ -73,33 +116,91 @@ __global__ __launch_bounds__(256) void fitness_partial_kernel(FitnessArgs f) {
     for (int i = 0; i < kBS; ++i)
 #pragma unroll
         for (int j = 0; j < kBS; ++j) g[i][j] = 0.0;
-    for (long long c0 = c_begin; c0 < c_begin + cpc; c0 += kCellsPerStage) {
-        for (int q = tid; q < kCellsPerStage * kCPR; q += 256) {
-            const int cell = q / kCPR, ch = q % kCPR;
-            const uint4 v = *reinterpret_cast<const uint4*>(
-                last + ((long long)b * cells + c0 + cell) * C + h * D + ch * kCE);
-            float* dst = sx + cell * D + ch * kCE;
-            if constexpr (sizeof(T) == 2) {
-                *reinterpret_cast<float4*>(dst) =
-                    make_float4(bf16lo(v.x), bf16hi(v.x), bf16lo(v.y), bf16hi(v.y));
-                *reinterpret_cast<float4*>(dst + 4) =
-                    make_float4(bf16lo(v.z), bf16hi(v.z), bf16lo(v.w), bf16hi(v.w));
+
+    double* mp = f.mom_part + ((long long)bh * f.chunks + chunk) * f.T * 3;
+    for (int tb = 0; tb < f.T; tb += kTB) {
+        const int tn = min(kTB, f.T - tb);  // states tb .. tb + tn - 1 in this pass
+        const bool last = tb + tn == f.T;
+        double s1[kTB], s2[kTB], pr[kTB];
+#pragma unroll
+        for (int k = 0; k < kTB; ++k) s1[k] = s2[k] = pr[k] = 0.0;
+        for (long long c0 = c_begin; c0 < c_begin + cpc; c0 += kCellsPerStage) {
+            const long long stage_off = (((long long)b * cells + c0) * (kHeads * D) + h * D) * (long long)sizeof(T);
+            uint4 x[kTB + 1][kPPT];  // states tb - 1 .. tb + kTB - 1
+            if (tb > 0) {
+                load_pieces<T, D, kPPT>(f, tb - 1, stage_off, tid, x[0]);
             } else {
-                *reinterpret_cast<uint4*>(dst) = v;
+#pragma unroll
+                for (int j = 0; j < kPPT; ++j) x[0][j] = make_uint4(0u, 0u, 0u, 0u);
+            }
+            // Past the last state the loads repeat it (cached); those sums are unused.
+#pragma unroll
+            for (int k = 0; k < kTB; ++k) load_pieces<T, D, kPPT>(f, min(tb + k, f.T - 1), stage_off, tid, x[k + 1]);
+#pragma unroll
+            for (int k = 0; k < kTB; ++k)
+#pragma unroll
+                for (int j = 0; j < kPPT; ++j) {
+                    float a[kCE], e[kCE];
+                    unpack_piece<T>(x[k][j], a);
+                    unpack_piece<T>(x[k + 1][j], e);
+#pragma unroll
+                    for (int u = 0; u < kCE; ++u) {
+                        const double va = a[u], vb = e[u];
+                        s1[k] += vb;
+                        s2[k] = __builtin_fma(vb, vb, s2[k]);
+                        pr[k] = __builtin_fma(va, vb, pr[k]);
+                    }
+                    // one piece at a time: the converted values stay few
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            if (last) {
+                // x[tn] holds the last state: stage it as fp32 for the Gram.
+#pragma unroll
+                for (int k = 1; k <= kTB; ++k) {
+                    if (k != tn) continue;
+#pragma unroll
+                    for (int j = 0; j < kPPT; ++j) {
+                        const int q = tid + 256 * j;
+                        if (kPieces % 256 == 0 || q < kPieces) {
+                            float e[kCE];
+                            unpack_piece<T>(x[k][j], e);
+                            float* dst = sx + (q / kCPR) * D + (q % kCPR) * kCE;
+#pragma unroll
+                            for (int u = 0; u < kCE; u += 4)
+                                *reinterpret_cast<float4*>(dst + u) = make_float4(e[u], e[u + 1], e[u + 2], e[u + 3]);
+                        }
+                    }
+                }
+                __syncthreads();
+                if (gact) {
+                    for (int cell = 0; cell < kCellsPerStage; ++cell) {
+                        const float4 xi = *reinterpret_cast<const float4*>(sx + cell * D + bi * kBS);
+                        const float4 xj = *reinterpret_cast<const float4*>(sx + cell * D + bj * kBS);
+                        const double di[4] = {xi.x, xi.y, xi.z, xi.w};
+                        const double dj[4] = {xj.x, xj.y, xj.z, xj.w};
+#pragma unroll
+                        for (int i = 0; i < kBS; ++i)
+#pragma unroll
+                            for (int j = 0; j < kBS; ++j) g[i][j] = __builtin_fma(di[i], dj[j], g[i][j]);
+                    }
+                }
+                __syncthreads();
+            }
+        }
+        // Block sums of this pass's states, in a fixed order (lanes, then waves).
+#pragma unroll
+        for (int k = 0; k < kTB; ++k) {
+            const double v[3] = {wave_sum_f64(s1[k]), wave_sum_f64(s2[k]), wave_sum_f64(pr[k])};
+            if (lane == 0) {
+                sred[wave][3 * k] = v[0];
+                sred[wave][3 * k + 1] = v[1];
+                sred[wave][3 * k + 2] = v[2];
             }
         }
         __syncthreads();
-        if (gact) {
-            for (int cell = 0; cell < kCellsPerStage; ++cell) {
-                const float4 xi = *reinterpret_cast<const float4*>(sx + cell * D + bi * kBS);
-                const float4 xj = *reinterpret_cast<const float4*>(sx + cell * D + bj * kBS);
-                const double di[4] = {xi.x, xi.y, xi.z, xi.w};
-                const double dj[4] = {xj.x, xj.y, xj.z, xj.w};
-#pragma unroll
-                for (int i = 0; i < kBS; ++i)
-#pragma unroll
-                    for (int j = 0; j < kBS; ++j) g[i][j] = __builtin_fma(di[i], dj[j], g[i][j]);
-            }
+        if (tid < 3 * tn) {
+            const double sum = sred[0][tid] + sred[1][tid] + sred[2][tid] + sred[3][tid];
+            mp[(long long)tb * 3 + tid] = (tb == 0 && tid == 2) ? 0.0 : sum;
         }
         __syncthreads();
     }
@@ -110,119 +211,162 @@ __global__ __launch_bounds__(256) void fitness_partial_kernel(FitnessArgs f) {
 #pragma unroll
             for (int j = 0; j < kBS; ++j) gp[(bi * kBS + i) * D + bj * kBS + j] = g[i][j];
     }
-
-    // ---- lag-1 moments over the whole history ---------------------------------------
-    // Per t = 1..T-1: sum a, sum b, sum ab, sum aa, sum bb with a = x_{t-1}, b = x_t.
-    const int npair = f.T - 1;
-    double* mp = f.mom_part + ((long long)bh * f.chunks + chunk) * npair * 5;
-    const long long nelem = cpc * D;
-    const long long base = ((long long)b * cells + c_begin) * C + h * D;
-    for (int t = 1; t < f.T; ++t) {
-        double sa = 0.0, sb = 0.0, sab = 0.0, saa = 0.0, sbb = 0.0;
-        const T* xa = history_state<T>(f, t - 1) + base;
-        const T* xb = history_state<T>(f, t) + base;
-        for (long long e = tid; e < nelem; e += 256) {
-            const long long off = (e / D) * C + (e % D);
-            const double va = Store<T>::to_f32(xa[off]);
-            const double vb = Store<T>::to_f32(xb[off]);
-            sa += va;
-            sb += vb;
-            sab = __builtin_fma(va, vb, sab);
-            saa = __builtin_fma(va, va, saa);
-            sbb = __builtin_fma(vb, vb, sbb);
-        }
-        const double vals[5] = {sa, sb, sab, saa, sbb};
-        const int lane = tid & 63, wave = tid >> 6;
-#pragma unroll
-        for (int m = 0; m < 5; ++m) {
-            const double w = wave_sum_f64(vals[m]);
-            if (lane == 0) sred[wave][m] = w;
-        }
-        __syncthreads();
-        if (tid < 5) mp[(t - 1) * 5 + tid] = sred[0][tid] + sred[1][tid] + sred[2][tid] + sred[3][tid];
-        __syncthreads();
-    }
 }
 
+// Value of v in lane l (l uniform), through two 32-bit lane reads.
+__device__ __forceinline__ double lane_f64(double v, int l) {
+    const unsigned long long b = __builtin_bit_cast(unsigned long long, v);
+    const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)b, l);
+    const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(b >> 32), l);
+    return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
+}
+
+// Keeps the compiler from moving LDS accesses across this point. The block is one
+// wave and LDS executes a wave's accesses in issue order, so program order is all
+// the ordering that one lane's write and another lane's later read need.
+__device__ __forceinline__ void lds_order() { asm volatile("" ::: "memory"); }
+
 // One wave per (batch, head): fixed-order reduction of the partials, the cyclic
-// two-sided Jacobi solve in fp64 LDS, then rank, coherence and fitness.
+// two-sided Jacobi solve in fp64, then rank, coherence and fitness.
 //
 // The solve visits the pairs (p, q) in the reference's cyclic row order
 // (failed_attempts/pseudopod.cu:391-436) and skips |a_pq| <= 1e-6. That absolute
 // threshold makes the converged diagonal depend on the visiting order when the
-// Gram is nearly singular, so the order is kept rather than a parallel one. In a
-// rotation the entries outside the 2x2 block (p, q) change only in rows p, q and
-// columns p, q, each read and written by one lane (lane i owns A[i][p], A[i][q],
-// A[p][i], A[q][i]), and the block itself takes its exact diagonal form; one
-// barrier per rotation publishes the new diagonal to the next rotation.
+// Gram is nearly singular, so the order is kept rather than a parallel one, and the
+// rotation chain is serial. Its latency is kept to the scalar arithmetic: lane i
+// holds column p (A[i][p]) and the diagonal (A[i][i]) in registers, so a_pq and
+// a_qq of the next pair are lane reads of registers rather than LDS round trips.
+// The matrix stays in LDS (exactly symmetric: each new value is written to both
+// (i, p) and (p, i)); column q is read from it once per rotation, in parallel with
+// the rotation's scalar chain, and column p once per row p. The chain's divisions
+// and square roots use the short correctly rounded forms of fp64.hpp, whose
+// preconditions every Gram of fp32 data meets.
+//
+// Skipped pairs cost no serial step: one ballot over column p finds the next pair
+// that rotates, and each lane keeps its own share of the off-diagonal sum, added
+// across lanes at the end of the sweep (the reference adds the same |a_pq| values
+// one by one in visiting order; the two sums can differ in their last bits, and
+// only their comparison with 1e-6 n is used). Since a pair at or below 1e-6 is
+// never rotated, that sum usually stays above 1e-6 n and the solve runs to its
+// 30-sweep limit, the last sweeps rotating nothing; a sweep that rotates nothing
+// ends the solve at once with the same matrix and sweep count.
 template <int D>
 __global__ __launch_bounds__(64) void fitness_finalize_kernel(FitnessArgs f) {
     constexpr int kLd = D + 1;  // padded row
     __shared__ double A[D * kLd];
-    __shared__ double sv[D];
     __shared__ double rho[64];
 
     const int bh = blockIdx.x, lane = threadIdx.x;
+    const bool own = D == kWave || lane < D;  // lane owns row/column `lane` of the matrix
     const double ncell = (double)f.G * f.G;
     const double tol = 1e-6;
 
-    // Fixed-order reduction of the Gram partials.
-    for (int e = lane; e < D * D; e += 64) {
-        double s = 0.0;
-        for (int c = 0; c < f.chunks; ++c) s += f.gram_part[((long long)bh * f.chunks + c) * D * D + e];
-        A[(e / D) * kLd + e % D] = s / ncell;
+    // Fixed-order reduction of the Gram partials: element e sums chunks 0, 1, ... in
+    // turn; kE elements per lane at once keep the loads independent.
+    {
+        constexpr int kE = D * D >= 4 * 64 ? 4 : D * D / 64;  // D * D is a multiple of 64
+        static_assert(D * D % (kE * 64) == 0, "whole groups of elements");
+        const double* gp = f.gram_part + (long long)bh * f.chunks * D * D;
+        for (int e0 = 0; e0 < D * D; e0 += kE * 64) {
+            double s[kE];
+#pragma unroll
+            for (int k = 0; k < kE; ++k) s[k] = 0.0;
+#pragma unroll 4
+            for (int c = 0; c < f.chunks; ++c)
+#pragma unroll
+                for (int k = 0; k < kE; ++k) s[k] += gp[(long long)c * D * D + e0 + k * 64 + lane];
+#pragma unroll
+            for (int k = 0; k < kE; ++k) {
+                const int e = e0 + k * 64 + lane;
+                A[(e / D) * kLd + e % D] = s[k] / ncell;
+            }
+        }
     }
     __syncthreads();
 
+    double diag = own ? A[lane * kLd + lane] : 0.0;
     int sweeps = 0;
     for (int sweep = 0; sweep < 30; ++sweep) {
         ++sweeps;
-        double off = 0.0;
-        for (int p = 0; p < D - 1; ++p)
-            for (int q = p + 1; q < D; ++q) {
-                const double app = A[p * kLd + p], aqq = A[q * kLd + q], apq = A[p * kLd + q];
-                off += fabs(apq);
-                if (fabs(apq) > tol) {  // uniform across the wave
-                    const double tau = (aqq - app) / (2.0 * apq);
-                    const double t = tau >= 0.0 ? 1.0 / (tau + sqrt(1.0 + tau * tau))
-                                                : -1.0 / (-tau + sqrt(1.0 + tau * tau));
-                    const double c = 1.0 / sqrt(1.0 + t * t), s = t * c;
-                    const int i = lane;
-                    if (i < D && i != p && i != q) {
-                        const double aip = A[i * kLd + p], aiq = A[i * kLd + q];
-                        A[i * kLd + p] = c * aip - s * aiq;
-                        A[i * kLd + q] = s * aip + c * aiq;
-                        const double api = A[p * kLd + i], aqi = A[q * kLd + i];
-                        A[p * kLd + i] = c * api - s * aqi;
-                        A[q * kLd + i] = s * api + c * aqi;
-                    }
-                    if (lane == 0) {
-                        A[p * kLd + p] = c * c * app + s * s * aqq - 2.0 * c * s * apq;
-                        A[q * kLd + q] = s * s * app + c * c * aqq + 2.0 * c * s * apq;
-                        A[p * kLd + q] = 0.0;
-                        A[q * kLd + p] = 0.0;
-                    }
-                    __syncthreads();
+        double offl = 0.0;  // lane q: sum over the rows p < q of |a_pq| when (p, q) is visited
+        bool rotated = false;
+        for (int p = 0; p < D - 1; ++p) {
+            lds_order();
+            double colp = own ? A[lane * kLd + p] : 0.0;  // A[lane][p] = a_p,lane
+            double app = lane_f64(diag, p);
+            for (int q = p + 1;;) {
+                // Pairs (p, q..) with |a_pq| <= tol are skipped without changing anything,
+                // so the next rotation is at the lowest lane >= q whose column-p entry
+                // exceeds tol; the skipped pairs only add their |a_pq| to the sum.
+                const bool ahead = own && lane >= q;
+                const unsigned long long m = __ballot(ahead && fabs(colp) > tol);
+                const int qn = m ? (int)__builtin_ctzll(m) : D;
+                if (ahead && lane <= qn) offl += fabs(colp);  // lane qn: the rotated pair's a_pq
+                if (qn >= D) break;
+                lds_order();
+                const double colq = own ? A[lane * kLd + qn] : 0.0;
+                const double apq = lane_f64(colp, qn);
+                const double aqq = lane_f64(diag, qn);
+                double c, s;
+                jacobi_rotation<true>(app, aqq, apq, c, s);
+                const double app_new = c * c * app + s * s * aqq - 2.0 * c * s * apq;
+                const double aqq_new = s * s * app + c * c * aqq + 2.0 * c * s * apq;
+                double np = c * colp - s * colq;
+                double nq = s * colp + c * colq;
+                if (lane == p) {
+                    np = app_new;
+                    nq = 0.0;
+                } else if (lane == qn) {
+                    np = 0.0;
+                    nq = aqq_new;
                 }
+                if (own) {
+                    A[lane * kLd + p] = np;
+                    A[p * kLd + lane] = np;
+                    A[lane * kLd + qn] = nq;
+                    A[qn * kLd + lane] = nq;
+                }
+                diag = lane == p ? app_new : (lane == qn ? aqq_new : diag);
+                colp = np;
+                app = app_new;
+                rotated = true;
+                q = qn + 1;
             }
+        }
+        const double off = wave_sum_f64(offl);
         if (off < tol * D) break;
+        // A sweep without a rotation leaves the matrix as it found it, so every later
+        // sweep repeats it exactly: the solve ends at the sweep limit.
+        if (!rotated) {
+            sweeps = 30;
+            break;
+        }
     }
+    lds_order();
 
-    // Coherence from the moment partials.
+    // Coherence from the per-state sums: pair t = (t - 1, t) has sum a = S1(t-1),
+    // sum b = S1(t), sum ab = P(t), sum aa = S2(t-1), sum bb = S2(t); chunks in order.
     const int npair = f.T - 1;
     const double n = ncell * D;
-    for (int t = lane; t < npair; t += 64) {
+    for (int t = lane + 1; t < f.T; t += 64) {
         double m[5] = {0, 0, 0, 0, 0};
-        for (int c = 0; c < f.chunks; ++c)
-            for (int j = 0; j < 5; ++j)
-                m[j] += f.mom_part[(((long long)bh * f.chunks + c) * npair + t) * 5 + j];
+        for (int c = 0; c < f.chunks; ++c) {
+            const double* q = f.mom_part + ((long long)bh * f.chunks + c) * f.T * 3;
+            m[0] += q[(t - 1) * 3];
+            m[1] += q[t * 3];
+            m[2] += q[t * 3 + 2];
+            m[3] += q[(t - 1) * 3 + 1];
+            m[4] += q[t * 3 + 1];
+        }
         const double cov = m[2] - m[0] * m[1] / n;
         const double va = m[3] - m[0] * m[0] / n;
         const double vb = m[4] - m[1] * m[1] / n;
         const double den = sqrt(fmax(va, 0.0) * fmax(vb, 0.0));
-        rho[t] = den > 0.0 ? cov / den : 0.0;
+        rho[t - 1] = den > 0.0 ? cov / den : 0.0;
     }
-    if (lane < D) sv[lane] = sqrt(fabs(A[lane * kLd + lane]));
+    double* sv = A;  // the matrix is no longer needed: its first row holds the singular values
+    __syncthreads();
+    if (own) sv[lane] = sqrt(fabs(diag));
     __syncthreads();
     if (lane == 0) {
         for (int i = 1; i < D; ++i) {  // descending insertion sort

@@ -82,7 +82,7 @@ struct FitnessArgs {
     long long t_stride; // bytes from state t to state t + 1 (may be negative)
     int T, B, G, D;
     double* gram_part;  // [B*H][chunks][D*D]
-    double* mom_part;   // [B*H][chunks][(T-1)*5]
+    double* mom_part;   // [B*H][chunks][T][3]: sum x_t, sum x_t^2, sum x_{t-1} x_t
     int chunks;
     float* erank;       // [B][H]
     float* coh;

@@ -5,7 +5,11 @@
 //     register-resident operands, with random or all-zero data (the matrix cores
 //     draw less power, and hold a higher clock, on zeros);
 //   * HBM: 16-byte-per-lane streaming read, write and copy kernels over 2 GiB.
+// It also checks on the device that the short fp64 division and square root of the
+// Jacobi rotation (fp64.hpp) return the bits of IEEE `/` and `sqrt`.
 #include <hip/hip_runtime.h>
+
+#include "fp64.hpp"
 
 #include <stdint.h>
 
@@ -81,6 +85,47 @@ uint32_t hash32(uint32_t x) {
     return x;
 }
 
+// splitmix64 finaliser: one 64-bit draw per (seed, index).
+__device__ uint64_t mix64(uint64_t z) {
+    z += 0x9e3779b97f4a7c15ULL;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ULL;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebULL;
+    return z ^ (z >> 31);
+}
+
+// A double with a uniform 52-bit mantissa, sign from bit 63 when `sign`, and a
+// binary exponent uniform in [lo, hi].
+__device__ double draw(uint64_t r, int lo, int hi, bool sign) {
+    const uint64_t e = (uint64_t)(1023 + lo + (int)((r >> 52) % (uint64_t)(hi - lo + 1)));
+    const uint64_t bits = (sign ? (r & 0x8000000000000000ULL) : 0ULL) | (e << 52) | (r & 0xFFFFFFFFFFFFFULL);
+    return __builtin_bit_cast(double, bits);
+}
+
+// Per index i: div_rn against / on (a, b) with exponents in [-60, 60], sqrt_ge1
+// against sqrt on x in [1, 2^120), and the whole rotation (c, s) against its IEEE
+// form on (app, aqq, apq) drawn like Gram entries, every eighth with app = aqq.
+__global__ void fp64_core_check(long long n, uint64_t seed, unsigned long long* bad) {
+    unsigned long long miss = 0;
+    for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x) {
+        const uint64_t r0 = mix64(seed ^ (uint64_t)(4 * i)), r1 = mix64(seed ^ (uint64_t)(4 * i + 1));
+        const uint64_t r2 = mix64(seed ^ (uint64_t)(4 * i + 2)), r3 = mix64(seed ^ (uint64_t)(4 * i + 3));
+        const double a = draw(r0, -60, 60, true), b = draw(r1, -60, 60, true);
+        if (__builtin_bit_cast(uint64_t, slime::div_rn(a, b)) != __builtin_bit_cast(uint64_t, a / b)) ++miss;
+        const double x = draw(r2, 0, 119, false);
+        if (__builtin_bit_cast(uint64_t, slime::sqrt_ge1(x)) != __builtin_bit_cast(uint64_t, sqrt(x))) ++miss;
+        const double app = draw(r0 ^ r3, -24, 8, false);
+        const double aqq = (i % 8 == 0) ? app : draw(r1 ^ r3, -24, 8, false);
+        const double apq = draw(r2 ^ (r3 << 7), -19, 8, true);  // |apq| > 1e-6 as in the solve
+        double c0, s0, c1, s1;
+        slime::jacobi_rotation<true>(app, aqq, apq, c0, s0);
+        slime::jacobi_rotation<false>(app, aqq, apq, c1, s1);
+        if (__builtin_bit_cast(uint64_t, c0) != __builtin_bit_cast(uint64_t, c1) ||
+            __builtin_bit_cast(uint64_t, s0) != __builtin_bit_cast(uint64_t, s1))
+            ++miss;
+    }
+    if (miss) atomicAdd(bad, miss);
+}
+
 }  // namespace
 
 extern "C" {
@@ -145,6 +190,21 @@ double slime_probe_hbm_gbs(int kind) {
     if (b) (void)hipFree(b);
     if (o) (void)hipFree(o);
     return best;
+}
+
+// Mismatches, out of 3 n comparisons, between the short fp64 division, square root
+// and rotation of fp64.hpp and their IEEE forms, over n seeded draws. -1 on error.
+long long slime_probe_fp64_core(long long n, unsigned long long seed) {
+    unsigned long long* bad = nullptr;
+    long long r = -1;
+    if (n > 0 && hipMalloc(&bad, 8) == hipSuccess && hipMemset(bad, 0, 8) == hipSuccess) {
+        hipLaunchKernelGGL(fp64_core_check, dim3(1024), dim3(256), 0, 0, n, (uint64_t)seed, bad);
+        unsigned long long h = 0;
+        if (hipGetLastError() == hipSuccess && hipMemcpy(&h, bad, 8, hipMemcpyDeviceToHost) == hipSuccess)
+            r = (long long)h;
+    }
+    if (bad) (void)hipFree(bad);
+    return r;
 }
 
 }  // extern "C"

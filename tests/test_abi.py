@@ -79,5 +79,6 @@ def test_probe_library_exports_the_ceiling_probes():
     lib = ctypes.CDLL(path)
     assert hasattr(lib, "slime_probe_mfma_tflops")
     assert hasattr(lib, "slime_probe_hbm_gbs")
+    assert hasattr(lib, "slime_probe_fp64_core")
     ca = _lib.load()
     assert not hasattr(ca, "slime_probe_mfma_tflops")
