@@ -76,10 +76,19 @@ __device__ __forceinline__ void st4(void* p, long long i, const float (&v)[4]) {
         *reinterpret_cast<float4*>(static_cast<float*>(p) + i) = make_float4(v[0], v[1], v[2], v[3]);
 }
 
+// d/dx GELU_tanh(x) = d/dx [x sigma(2u)], u = c0 (x + c1 x^3):
+//   sigma + 2 x sigma (1 - sigma) u',  u' = c0 (1 + 3 c1 x^2),
+// the tanh form 0.5 (1 + th) + 0.5 x (1 - th^2) u' with th = 2 sigma - 1. With
+// e = exp(-2u), sigma = 1 / (1 + e) and 1 - sigma = e sigma, so nothing cancels;
+// the exponent is capped at 2^126, where sigma and the second term are negligible.
 __device__ __forceinline__ float gelu_grad(float x) {
-    const float c0 = 0.7978845608028654f, c1 = 0.044715f;
-    const float th = tanhf(c0 * (x + c1 * x * x * x));
-    return 0.5f * (1.0f + th) + 0.5f * x * (1.0f - th * th) * c0 * (1.0f + 3.0f * c1 * x * x);
+    constexpr float c0 = 0.7978845608028654f, c1 = 0.044715f, kLog2e = 1.4426950408889634f;
+    const float x2 = x * x;
+    const float u = c0 * x * __builtin_fmaf(c1, x2, 1.0f);
+    const float e = exp2_fast(fminf(-2.0f * kLog2e * u, 126.0f));
+    const float sg = rcp_fast(1.0f + e);
+    const float du = c0 * __builtin_fmaf(3.0f * c1, x2, 1.0f);
+    return sg * __builtin_fmaf(2.0f * x * du, e * sg, 1.0f);
 }
 
 // ---- S7: loss, Q_o, B_o partial sums ---------------------------------------------------
@@ -237,14 +246,14 @@ __global__ __launch_bounds__(256) void bw_cell_kernel(BackwardArgs a) {
             mu = a.mu[pod * H + h];
             sg = a.sigma[pod * H + h];
         }
-        const float sp = sg + 1e-7f;
+        const float inv_sp = 1.0f / (sg + 1e-7f);
         float t[4], et[4], g[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             float u = 0.f;
 #pragma unroll
             for (int k = 0; k < 9; ++k) u = __builtin_fmaf(kw[k], xk[k].v[e], u);
-            t[e] = (u - mu) / sp;
+            t[e] = (u - mu) * inv_sp;
             et[e] = __expf(-t[e] * t[e]);
             g[e] = 2.0f * et[e] - 1.0f;
         }
@@ -263,10 +272,11 @@ __global__ __launch_bounds__(256) void bw_cell_kernel(BackwardArgs a) {
             s[k] = __expf(s[k] - mx);
             den += s[k];
         }
+        const float rden = 1.0f / den;
         float vt[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int k = 0; k < 9; ++k) {
-            s[k] /= den;  // a_k
+            s[k] *= rden;  // a_k
 #pragma unroll
             for (int e = 0; e < 4; ++e) vt[e] = __builtin_fmaf(s[k], vk[k].v[e], vt[e]);
         }
@@ -294,7 +304,7 @@ __global__ __launch_bounds__(256) void bw_cell_kernel(BackwardArgs a) {
         for (int e = 0; e < 4; ++e) {
             const float gg = dt * gz[e] * vt[e];
             gvt[e] = dt * gz[e] * g[e];
-            gu[e] = gg * (-4.0f * t[e] * et[e]) / sp;
+            gu[e] = gg * (-4.0f * t[e] * et[e]) * inv_sp;
             gmu_l -= gu[e];
             gsg_l -= gu[e] * t[e];
         }
@@ -371,43 +381,73 @@ template <typename T, int kD>
 __global__ __launch_bounds__(256) void bw_gather_kernel(BackwardArgs a) {
     constexpr int H = kHeads, C = H * kD;
     const int G = a.G;
-    const long long cells = (long long)G * G;
-    const long long e4 = (long long)blockIdx.x * 256 + threadIdx.x;  // 4-channel unit
-    if (e4 * 4 >= (long long)a.B * cells * C) return;
-    const long long e = e4 * 4;
-    const long long q = e / C;
-    const int ch = (int)(e % C), h = ch / kD;
-    const int b = (int)(q / cells);
-    const long long cell = q % cells;
-    const int y = (int)(cell / G), x = (int)(cell % G);
-    const int pod = b / a.per_pod;
+    // Element offsets fit in 32 bits: the state holds at most 4e9 elements.
+    const unsigned cells = (unsigned)G * (unsigned)G;
+    const unsigned e4 = blockIdx.x * 256u + threadIdx.x;  // 4-channel unit
+    if ((unsigned long long)e4 * 4 >= (unsigned long long)a.B * cells * C) return;
+    const unsigned e = e4 * 4;
+    const unsigned q = e4 / (C / 4);
+    const int ch = (int)(e4 % (C / 4)) * 4, h = ch / kD;
+    const unsigned b = q / cells;
+    const unsigned cell = q - b * cells;
+    const int y = (int)(cell / (unsigned)G), x = (int)(cell - (unsigned)y * (unsigned)G);
+    const int pod = (int)b / a.per_pod;
     const float inv_sqrt_d = 1.0f / __builtin_sqrtf((float)kD);
-    float gv[4] = {0.f, 0.f, 0.f, 0.f}, gi[4] = {0.f, 0.f, 0.f, 0.f}, gx[4] = {0.f, 0.f, 0.f, 0.f};
+    // All 9 neighbours' loads are issued before any use, so they are in flight together:
+    // the empty asm statements (memory clobber) keep every load above them and take
+    // the loaded registers as operands, so no arithmetic starts before the last load.
+    float ak[9], gs[9], kw[9];
+    f32x4 gvt[9], gu[9];
+    u32x2 prw[9];
 #pragma unroll
     for (int k = 0; k < 9; ++k) {
-        const long long r = (long long)b * cells + (long long)wrapb(y - (k / 3 - 1), G) * G +
-                            wrapb(x - (k % 3 - 1), G);
-        const long long ir = r * C + ch;
-        const float ak = a.att[(r * H + h) * 9 + k], gs = a.gS[(r * H + h) * 9 + k] * inv_sqrt_d;
-        const float kk = a.K[(pod * H + h) * 9 + k];
-        const F4 gvt = ld4f(a.gVt, ir), pr = ld4<T>(a.P, ir), gu = ld4f(a.gU, ir);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            gv[j] = __builtin_fmaf(ak, gvt.v[j], gv[j]);
-            gi[j] = __builtin_fmaf(gs, pr.v[j], gi[j]);
-            gx[j] = __builtin_fmaf(kk, gu.v[j], gx[j]);
-        }
+        const unsigned r = b * cells + (unsigned)(wrapb(y - (k / 3 - 1), G) * G + wrapb(x - (k % 3 - 1), G));
+        const unsigned ir = r * C + ch;
+        const unsigned long long ai = ((unsigned long long)r * H + h) * 9 + k;  // may pass 2^32
+        kw[k] = a.K[(pod * H + h) * 9 + k];
+        ak[k] = a.att[ai];
+        gs[k] = a.gS[ai];
+        gvt[k] = *reinterpret_cast<const f32x4*>(a.gVt + ir);
+        gu[k] = *reinterpret_cast<const f32x4*>(a.gU + ir);
+        if constexpr (sizeof(T) == 2)
+            prw[k] = *reinterpret_cast<const u32x2*>(static_cast<const T*>(a.P) + ir);
     }
     const F4 ip = ld4<T>(a.Ipre, e);
     const F4 gd = ld4f(a.gXd, e);
+#pragma unroll
+    for (int k = 0; k < 9; ++k) {
+        if constexpr (sizeof(T) == 2)
+            asm volatile("" : "+v"(gvt[k]), "+v"(gu[k]), "+v"(prw[k]), "+v"(ak[k]), "+v"(gs[k]), "+v"(kw[k])::"memory");
+        else
+            asm volatile("" : "+v"(gvt[k]), "+v"(gu[k]), "+v"(ak[k]), "+v"(gs[k]), "+v"(kw[k])::"memory");
+    }
+    float gv[4] = {0.f, 0.f, 0.f, 0.f}, gi[4] = {0.f, 0.f, 0.f, 0.f}, gx[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < 9; ++k) {
+        F4 pr;
+        if constexpr (sizeof(T) == 2) {
+            pr = F4{{bf16lo(prw[k].x), bf16hi(prw[k].x), bf16lo(prw[k].y), bf16hi(prw[k].y)}};
+        } else {
+            const unsigned r = b * cells + (unsigned)(wrapb(y - (k / 3 - 1), G) * G + wrapb(x - (k % 3 - 1), G));
+            pr = ld4<T>(a.P, r * C + ch);
+        }
+        const float gsk = gs[k] * inv_sqrt_d;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            gv[j] = __builtin_fmaf(ak[k], gvt[k][j], gv[j]);
+            gi[j] = __builtin_fmaf(gsk, pr.v[j], gi[j]);
+            gx[j] = __builtin_fmaf(kw[k], gu[k][j], gx[j]);
+        }
+    }
     float g1[4], gxd[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         g1[j] = gi[j] * gelu_grad(ip.v[j]);
         gxd[j] = gd.v[j] + gx[j];
     }
-    st4<T>(a.G3, q * 3 * C + C + ch, g1);
-    st4<T>(a.G3, q * 3 * C + 2 * C + ch, gv);
+    const long long g3 = (long long)q * 3 * C + ch;  // G3 holds three planes: past 2^32
+    st4<T>(a.G3, g3 + C, g1);
+    st4<T>(a.G3, g3 + 2 * C, gv);
     st4f(a.gXd, e, gxd);
 }
 
