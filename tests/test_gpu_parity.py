@@ -305,6 +305,26 @@ def test_fitness_matches_oracle(oracle, dtype, D):
     np.testing.assert_allclose(fit, rfit, rtol=1e-6, atol=1e-6)
 
 
+@pytest.mark.parametrize("T", [9, 11, 17])
+def test_fitness_long_history_matches_oracle(oracle, T):
+    """Histories longer than the 8 states one pass of the partial kernel reads: the
+    later passes start from the previous pass's last state."""
+    cfg = _cfg("fitT", B=1, G=16, D=32, dtype="fp32")
+    rng = np.random.default_rng(T)
+    X = make_state(cfg, seed=3)
+    hist_h = np.stack([X + 0.05 * t * rng.standard_normal(X.shape).astype(np.float32)
+                       for t in range(T)]).astype(np.float32)
+    with _engine(cfg) as e:
+        er, coh, fit = e.fitness(torch.from_numpy(hist_h).cuda().contiguous())
+        torch.cuda.synchronize()
+        er, coh, fit = _host(er), _host(coh), _host(fit)
+    rer, rcoh, rfit = oracle.fitness(_ocfg(cfg), hist_h)
+    print(f"  T={T}: coh {coh.ravel()[:3]} oracle {rcoh.ravel()[:3]}")
+    np.testing.assert_allclose(er, rer, rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(coh, rcoh, atol=1e-6)
+    np.testing.assert_allclose(fit, rfit, rtol=1e-6, atol=1e-6)
+
+
 @pytest.mark.parametrize("kind", ["diagonal", "rank1", "rank1_plus_noise"])
 def test_fitness_sweep_paths(oracle, kind):
     """The three ways the solve ends, against the oracle's sweep counts and ranks: a
