@@ -555,36 +555,49 @@ hipError_t launch_gemm(int dtype, const GemmArgs& a, hipStream_t s) {
 
 // ---- weight preparation --------------------------------------------------------------
 namespace {
+constexpr int kPrepBatches = 8;  // batches per thread
+
+// One thread per 8 consecutive k of one (plane, n) row of one pod's masters (the 8
+// share a head: D >= 8) and up to kPrepBatches batches of that pod (grid y): the
+// masters are read once per thread, and each batch's scaled copy leaves as one
+// 16-byte (bf16) or two 16-byte (fp32) stores.
 template <typename T>
 __global__ __launch_bounds__(256) void weight_prep_kernel(WeightPrepArgs w) {
-    // Four consecutive k per thread: coalesced fp32 reads, 8/16-byte writes.
     const long long per_b = (long long)w.nplanes * w.C * w.C;
     const long long q = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (q * 4 >= per_b * w.B) return;
-    const long long idx = q * 4;
-    const int b = (int)(idx / per_b);
-    const long long r = idx - (long long)b * per_b;
+    const int pods = w.B / w.per_pod;
+    if (q * 8 >= per_b * pods) return;
+    const int pod = (int)(q * 8 / per_b);
+    const long long r = q * 8 - (long long)pod * per_b;
     const int k = (int)(r % w.C);
     const int p = (int)(r / ((long long)w.C * w.C));
-    const int pod = b / w.per_pod;
-    float4 v = *reinterpret_cast<const float4*>(w.Wtm + (long long)pod * per_b + r);
-    if (w.scale && ((w.scaled_planes >> p) & 1u)) {
-        const float s = w.scale[b * (w.C / w.D) + k / w.D];  // 4 k share one head (D >= 8)
-        v.x *= s;
-        v.y *= s;
-        v.z *= s;
-        v.w *= s;
+    const float* src = w.Wtm + (long long)pod * per_b + r;
+    const float4 v0 = *reinterpret_cast<const float4*>(src);
+    const float4 v1 = *reinterpret_cast<const float4*>(src + 4);
+    const bool scaled = w.scale && ((w.scaled_planes >> p) & 1u);
+    const int heads = w.C / w.D, head = k / w.D;
+    const int b0 = blockIdx.y * kPrepBatches;
+    const int b1 = min(w.per_pod, b0 + kPrepBatches);
+#pragma unroll 4
+    for (int bb = b0; bb < b1; ++bb) {
+        const int b = pod * w.per_pod + bb;
+        const float s = scaled ? w.scale[b * heads + head] : 1.0f;
+        if constexpr (sizeof(T) == 2) {
+            *reinterpret_cast<uint4*>(static_cast<T*>(w.Wt) + (long long)b * per_b + r) =
+                make_uint4(pack_bf16x2(v0.x * s, v0.y * s), pack_bf16x2(v0.z * s, v0.w * s),
+                           pack_bf16x2(v1.x * s, v1.y * s), pack_bf16x2(v1.z * s, v1.w * s));
+        } else {
+            float* dst = static_cast<float*>(w.Wt) + (long long)b * per_b + r;
+            *reinterpret_cast<float4*>(dst) = make_float4(v0.x * s, v0.y * s, v0.z * s, v0.w * s);
+            *reinterpret_cast<float4*>(dst + 4) = make_float4(v1.x * s, v1.y * s, v1.z * s, v1.w * s);
+        }
     }
-    if constexpr (sizeof(T) == 2)
-        reinterpret_cast<uint2*>(w.Wt)[q] = make_uint2(pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w));
-    else
-        reinterpret_cast<float4*>(w.Wt)[q] = v;
 }
 }  // namespace
 
 hipError_t launch_weight_prep(int dtype, const WeightPrepArgs& a, hipStream_t s) {
-    const long long quads = (long long)a.B * a.nplanes * a.C * a.C / 4;
-    const dim3 grid((unsigned)((quads + 255) / 256));
+    const long long units = (long long)(a.B / a.per_pod) * a.nplanes * a.C * a.C / 8;
+    const dim3 grid((unsigned)((units + 255) / 256), (unsigned)((a.per_pod + kPrepBatches - 1) / kPrepBatches));
     if (dtype == 1)
         hipLaunchKernelGGL(weight_prep_kernel<bf16_t>, grid, dim3(256), 0, s, a);
     else
