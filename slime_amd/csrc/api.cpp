@@ -616,7 +616,7 @@ int slime_ca_backward(slime_ca* h, const void* x_in, const void* target, float* 
     const size_t C = h->C, BH = (size_t)c.B * c.H, n = (size_t)h->state_elems;
     const size_t cells = (size_t)c.B * c.G * c.G;
     const int lchunks = backward_loss_chunks(c.G);
-    const int nW = 128;
+    const int nW = 1024;  // cell-pass workgroups per pod
     const long long rows_pod = (long long)(c.B / c.pods) * c.G * c.G;
     const int dw_chunks = backward_dw_chunks_per_pod(c.dtype, (int)C, rows_pod);
     const bool want_w = grads && (grads->WP || grads->WI || grads->WV);

@@ -173,11 +173,14 @@ __global__ __launch_bounds__(256) void bw_loss_finalize_kernel(BackwardArgs a) {
 }
 
 // ---- per (cell, head): S7, S6, S3, S5, S4 backward and the tape for the gathers ------------
-// Block (pod, head, w): each group of kL = D/4 lanes owns one (cell, head), a lane 4
-// consecutive channels (8- or 16-byte loads), and the per-(cell, head) dot products
-// reduce over the group with DPP lane moves. Group g handles cells i = w*groups + g
-// (+ stride) of the pod's batches. Per-thread parameter partials (M column h, K row
-// h, mu, sigma) are reduced over the block and written once.
+// Block (pod, w) walks cells w*kCpi .. +kCpi-1 (+ stride) of the pod's batches with all
+// eight heads of each cell: group g of kL = D/4 lanes owns (cell slot g / 8, head
+// g % 8), a lane 4 consecutive channels (8- or 16-byte loads), and the per-(cell,
+// head) dot products reduce over the group with DPP lane moves. Each lane computes
+// the loss gradient gY of its own head's 4 channels once and shares it through LDS,
+// where every head of the cell reads the 8 output heads it mixes from (S6). Per-thread
+// parameter partials (M column h, K row h, mu, sigma) are reduced per head over the
+// block and written once.
 constexpr int kPartF = kHeads + 9 + 2;  // gM[o][h] (8), gK[h][k] (9), gmu, gsigma
 
 // Sum over groups of kL adjacent lanes (kL = 2 .. 16, inside one 16-lane DPP row),
@@ -193,15 +196,18 @@ __device__ __forceinline__ float lanes_sum(float v) {
 
 template <typename T, int kD>
 __global__ __launch_bounds__(256) void bw_cell_kernel(BackwardArgs a) {
-    constexpr int H = kHeads, C = H * kD, kL = kD / 4, kGroups = 256 / kL;
+    constexpr int H = kHeads, C = H * kD, kL = kD / 4, kGroups = 256 / kL, kCpi = kGroups / H;
     static_assert(kL >= 2 && kL <= 16, "4 channels per lane, groups inside a DPP row");
+    __shared__ __attribute__((aligned(16))) float sgy[kCpi * C];  // gY of the block's cells
     const int G = a.G;
     const long long cells = (long long)G * G;
     const int w = blockIdx.x % a.nW;
-    const int h = (blockIdx.x / a.nW) % H;
-    const int pod = blockIdx.x / (a.nW * H);
+    const int pod = blockIdx.x / a.nW;
     const int grp = threadIdx.x / kL, li = threadIdx.x % kL;
+    const int cs = grp / H, h = grp % H;
     const int c0 = 4 * li;
+    // A multiple of kCpi (G is a multiple of 8), so every slot of an iteration is a cell
+    // and all threads of the block run the same iterations (they meet at barriers).
     const long long pod_cells = (long long)a.per_pod * cells;
     const float inv_sqrt_d = 1.0f / __builtin_sqrtf((float)kD);
     const float dt = a.dt;
@@ -217,7 +223,8 @@ __global__ __launch_bounds__(256) void bw_cell_kernel(BackwardArgs a) {
 #pragma unroll
     for (int k = 0; k < 9; ++k) pK[k] = 0.f;
 
-    for (long long i = (long long)w * kGroups + grp; i < pod_cells; i += (long long)a.nW * kGroups) {
+    for (long long i0 = (long long)w * kCpi; i0 < pod_cells; i0 += (long long)a.nW * kCpi) {
+        const long long i = i0 + cs;
         const int b = pod * a.per_pod + (int)(i / cells);
         const long long cell = i % cells;
         const int y = (int)(cell / G), x = (int)(cell % G);
@@ -237,6 +244,7 @@ __global__ __launch_bounds__(256) void bw_cell_kernel(BackwardArgs a) {
             vk[k] = ld4<T>(a.V, nb[k]);
         }
         const F4 pc = ld4<T>(a.P, ir);
+        const F4 yv = ld4f(a.Y, ir), tv = ld4<T>(a.T, ir);  // output head h of this cell
         float mu, sg;
         if (a.per_cell) {
             const long long pi = ((long long)pod * cells + cell) * H + h;
@@ -283,21 +291,28 @@ __global__ __launch_bounds__(256) void bw_cell_kernel(BackwardArgs a) {
         float z[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) z[e] = __builtin_fmaf(dt * g[e], vt[e], xk[4].v[e]);
-        // ---- S7 -> gY for every output head o at (r, c0..c0+3); S6 -> gZ_h ----
+        // ---- S7 -> gY of output head h at (r, c0..c0+3), shared; S6 -> gZ_h ----
+        {
+            const float rs = a.scale[b * H + h];
+            const float cy = a.coef[(b * H + h) * 2], cq = a.coef[(b * H + h) * 2 + 1];
+            float gyo[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) gyo[e] = cy * (2.0f * (rs * yv.v[e] - tv.v[e]) * a.inv_n - cq);
+            *reinterpret_cast<float4*>(sgy + cs * C + h * kD + c0) = make_float4(gyo[0], gyo[1], gyo[2], gyo[3]);
+        }
+        __syncthreads();
         float gz[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int o = 0; o < H; ++o) {
-            const long long io = r * C + o * kD + c0;
-            const float rs = a.scale[b * H + o];
-            const float cy = a.coef[(b * H + o) * 2], cq = a.coef[(b * H + o) * 2 + 1];
-            const F4 yv = ld4f(a.Y, io), tv = ld4<T>(a.T, io);
+            const float4 gq = *reinterpret_cast<const float4*>(sgy + cs * C + o * kD + c0);
+            const float gy[4] = {gq.x, gq.y, gq.z, gq.w};
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const float gy = cy * (2.0f * (rs * yv.v[e] - tv.v[e]) * a.inv_n - cq);
-                gz[e] = __builtin_fmaf(mcol[o], gy, gz[e]);
-                pM[o] = __builtin_fmaf(gy, z[e], pM[o]);
+                gz[e] = __builtin_fmaf(mcol[o], gy[e], gz[e]);
+                pM[o] = __builtin_fmaf(gy[e], z[e], pM[o]);
             }
         }
+        __syncthreads();  // sgy is rewritten by the next iteration
         // ---- S6, S3 ----
         float gu[4], gvt[4], gmu_l = 0.f, gsg_l = 0.f;
 #pragma unroll
@@ -365,13 +380,15 @@ __global__ __launch_bounds__(256) void bw_cell_kernel(BackwardArgs a) {
     red[H + 9][threadIdx.x] = pmu;
     red[H + 10][threadIdx.x] = psg;
     __syncthreads();
-    for (int s2 = 128; s2 > 0; s2 >>= 1) {
-        if ((int)threadIdx.x < s2)
-            for (int q = 0; q < kPartF; ++q) red[q][threadIdx.x] += red[q][threadIdx.x + s2];
-        __syncthreads();
+    // per head h: the threads of groups g = cs * H + h, in the order (cs, lane)
+    if ((int)threadIdx.x < H * kPartF) {
+        const int hh = threadIdx.x / kPartF, q = threadIdx.x % kPartF;
+        float sum = 0.f;
+        for (int c2 = 0; c2 < kCpi; ++c2)
+#pragma unroll
+            for (int l2 = 0; l2 < kL; ++l2) sum += red[q][(c2 * H + hh) * kL + l2];
+        a.ppart[((long long)(pod * H + hh) * a.nW + w) * kPartF + q] = sum;
     }
-    if ((int)threadIdx.x < kPartF)
-        a.ppart[(long long)blockIdx.x * kPartF + threadIdx.x] = red[threadIdx.x][0];
 }
 
 // ---- gathers: gV, gI~ (planes 2 and 1 of G3) and the potential's transpose -------------------
@@ -452,14 +469,23 @@ __global__ __launch_bounds__(256) void bw_gather_kernel(BackwardArgs a) {
 }
 
 // ---- parameter finalize: fixed-order sums of the per-block partials ----------------------------
-__global__ __launch_bounds__(64) void bw_param_finalize_kernel(BackwardArgs a) {
-    // one thread per (pod, head, quantity)
-    const int idx = blockIdx.x * 64 + threadIdx.x;
-    if (idx >= a.pods * kHeads * kPartF) return;
+__global__ __launch_bounds__(256) void bw_param_finalize_kernel(BackwardArgs a) {
+    // one block per (pod, head, quantity): thread t adds partials t, t + 256, ... in
+    // order, then a fixed tree adds the 256 sums
+    __shared__ float sm[256];
+    const int idx = blockIdx.x;
     const int q = idx % kPartF, h = (idx / kPartF) % kHeads, pod = idx / (kPartF * kHeads);
+    const float* src = a.ppart + (long long)(pod * kHeads + h) * a.nW * kPartF + q;
     float sum = 0.f;
-    for (int w = 0; w < a.nW; ++w)
-        sum += a.ppart[((long long)(pod * kHeads + h) * a.nW + w) * kPartF + q];
+    for (int w = threadIdx.x; w < a.nW; w += 256) sum += src[(long long)w * kPartF];
+    sm[threadIdx.x] = sum;
+    __syncthreads();
+    for (int s2 = 128; s2 > 0; s2 >>= 1) {
+        if ((int)threadIdx.x < s2) sm[threadIdx.x] += sm[threadIdx.x + s2];
+        __syncthreads();
+    }
+    if (threadIdx.x != 0) return;
+    sum = sm[0];
     if (q < kHeads) {
         if (a.gM) a.gM[(pod * kHeads + q) * kHeads + h] = sum;  // gM[o = q][h]
     } else if (q < kHeads + 9) {
@@ -689,10 +715,9 @@ hipError_t launch_dt(const BackwardArgs& a, hipStream_t s) {
     const long long n = (long long)a.B * cells * kHeads * kD;
     hipLaunchKernelGGL((bw_loss_partial_kernel<T>), dim3(a.lchunks, a.B), dim3(256), 0, s, a);
     hipLaunchKernelGGL(bw_loss_finalize_kernel, dim3(a.B * kHeads), dim3(256), 0, s, a);
-    hipLaunchKernelGGL((bw_cell_kernel<T, kD>), dim3(a.pods * kHeads * a.nW), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((bw_cell_kernel<T, kD>), dim3(a.pods * a.nW), dim3(256), 0, s, a);
     hipLaunchKernelGGL((bw_gather_kernel<T, kD>), dim3((unsigned)((n / 4 + 255) / 256)), dim3(256), 0, s, a);
-    hipLaunchKernelGGL(bw_param_finalize_kernel, dim3((a.pods * kHeads * kPartF + 63) / 64), dim3(64), 0,
-                       s, a);
+    hipLaunchKernelGGL(bw_param_finalize_kernel, dim3(a.pods * kHeads * kPartF), dim3(256), 0, s, a);
     if (a.per_cell)
         hipLaunchKernelGGL(bw_cell_param_finalize_kernel,
                            dim3((unsigned)((a.pods * cells * kHeads + 255) / 256)), dim3(256), 0, s, a);

@@ -122,7 +122,7 @@ struct BackwardArgs {
     void* G3;                // [B][G][G][3C] gradients of P~, I~, V (storage type)
     float* gXd;              // [B][G][G][C] direct part of dL/dX
     float* ppart;            // [pods][H][nW][backward_part_floats()]
-    int nW;                  // workgroups per (pod, head) in the cell pass
+    int nW;                  // workgroups per pod in the cell pass
     float* gcell;            // per-cell growth: [B][G][G][H][2]
     // outputs (device, fp32, parameter layouts; may be nullptr)
     float* gK;
