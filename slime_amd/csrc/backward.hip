@@ -705,8 +705,19 @@ __global__ __launch_bounds__(256) void bw_dw_reduce_kernel(DwArgs d) {
 template <typename T>
 __global__ __launch_bounds__(256) void bw_final_kernel(const float* gXd, const void* gXp, float* gX,
                                                        long long n) {
-    const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
-    if (i < n) gX[i] = gXd[i] + ld<T>(gXp, i);
+    // 8 elements per thread (n is a multiple of 8: C >= 64)
+    const long long i = ((long long)blockIdx.x * 256 + threadIdx.x) * 8;
+    if (i >= n) return;
+    const F4 d0 = ld4f(gXd, i), d1 = ld4f(gXd, i + 4);
+    const F4 p0 = ld4<T>(gXp, i), p1 = ld4<T>(gXp, i + 4);
+    float r0[4], r1[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        r0[e] = d0.v[e] + p0.v[e];
+        r1[e] = d1.v[e] + p1.v[e];
+    }
+    st4f(gX, i, r0);
+    st4f(gX, i + 4, r1);
 }
 
 template <typename T, int kD>
@@ -771,7 +782,7 @@ hipError_t launch_backward_dw(int dtype, const BackwardArgs& a, const DwArgs& d,
 
 hipError_t launch_backward_final(int dtype, const float* gXd, const void* gXp, float* gX, long long n,
                                  hipStream_t s) {
-    const dim3 grid((unsigned)((n + 255) / 256));
+    const dim3 grid((unsigned)((n / 8 + 255) / 256));
     if (dtype == 1)
         hipLaunchKernelGGL((bw_final_kernel<bf16_t>), grid, dim3(256), 0, s, gXd, gXp, gX, n);
     else
