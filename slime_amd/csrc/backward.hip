@@ -468,6 +468,109 @@ __global__ __launch_bounds__(256) void bw_gather_kernel(BackwardArgs a) {
     st4f(a.gXd, e, gxd);
 }
 
+// ---- gathers for D = 64 through an LDS halo tile -----------------------------------------------
+// The same sums as bw_gather_kernel, in the same order (k = 0..8), for one 4 x 8 cell
+// tile of one (batch, head) per workgroup: the tile's 6 x 10 halo of gVt, gU (fp32),
+// P (storage type) and the tape (a_k, gs_k) is read into LDS once, so each halo value
+// crosses L2 once per tile instead of once per neighbour that uses it. Thread t owns
+// cell t / 8 of the tile and channels 8 (t % 8) .. +7.
+constexpr int kGTy = 4, kGTx = 8, kGHx = kGTx + 2, kGHalo = (kGTy + 2) * kGHx;  // 60 halo cells
+constexpr int kGRowF = 68;  // floats per staged fp32 row (64 + 4: rows of a wave on distinct banks)
+
+template <typename T>
+__global__ __launch_bounds__(256) void bw_gather_tile_kernel(BackwardArgs a) {
+    constexpr int H = kHeads, kD = 64, C = H * kD;
+    __shared__ __attribute__((aligned(16))) float sV[kGHalo * kGRowF];   // gVt
+    __shared__ __attribute__((aligned(16))) float sU[kGHalo * kGRowF];   // gU
+    __shared__ __attribute__((aligned(16))) float sP[kGHalo * kGRowF];   // P, widened
+    __shared__ float sA[kGHalo * 9], sS[kGHalo * 9];                     // a_k, gs_k
+    const int G = a.G;
+    const int tiles_x = G / kGTx, tpb = (G / kGTy) * tiles_x;
+    const int h = blockIdx.x % H;
+    const int tile = (blockIdx.x / H) % tpb;
+    const int b = blockIdx.x / (H * tpb);
+    const int ty0 = (tile / tiles_x) * kGTy, tx0 = (tile % tiles_x) * kGTx;
+    const long long cells = (long long)G * G;
+    const long long bcell = (long long)b * cells;
+    const int tid = threadIdx.x;
+    // ---- stage the halo: 60 cells x 64 channels, 4 channels per lane-step (the first
+    // three steps cover every lane, so their loads are in flight together) ----
+#pragma unroll
+    for (int it = 0; it < (kGHalo * (kD / 4) + 255) / 256; ++it) {
+        const int e = tid + 256 * it;
+        if (256 * (it + 1) > kGHalo * (kD / 4) && e >= kGHalo * (kD / 4)) break;
+        const int hc = e / (kD / 4), c4 = (e % (kD / 4)) * 4;
+        const int gy = wrapb(ty0 + hc / kGHx - 1, G), gx = wrapb(tx0 + hc % kGHx - 1, G);
+        const long long ir = (bcell + (long long)gy * G + gx) * C + h * kD + c4;
+        *reinterpret_cast<float4*>(sV + hc * kGRowF + c4) = *reinterpret_cast<const float4*>(a.gVt + ir);
+        *reinterpret_cast<float4*>(sU + hc * kGRowF + c4) = *reinterpret_cast<const float4*>(a.gU + ir);
+        const F4 pv = ld4<T>(a.P, ir);
+        *reinterpret_cast<float4*>(sP + hc * kGRowF + c4) = make_float4(pv.v[0], pv.v[1], pv.v[2], pv.v[3]);
+    }
+    for (int e = tid; e < kGHalo * 9; e += 256) {
+        const int hc = e / 9, k = e % 9;
+        const int gy = wrapb(ty0 + hc / kGHx - 1, G), gx = wrapb(tx0 + hc % kGHx - 1, G);
+        const long long ai = ((bcell + (long long)gy * G + gx) * H + h) * 9 + k;
+        sA[e] = a.att[ai];
+        sS[e] = a.gS[ai];
+    }
+    const int cell = tid / 8, c0 = 8 * (tid % 8);
+    const int cy = cell / kGTx, cx = cell % kGTx;
+    const long long q = bcell + (long long)(ty0 + cy) * G + tx0 + cx;
+    const long long e0 = q * C + h * kD + c0;
+    const F4 ip0 = ld4<T>(a.Ipre, e0), ip1 = ld4<T>(a.Ipre, e0 + 4);
+    const F4 gd0 = ld4f(a.gXd, e0), gd1 = ld4f(a.gXd, e0 + 4);
+    const int pod = b / a.per_pod;
+    float kw[9];
+#pragma unroll
+    for (int k = 0; k < 9; ++k) kw[k] = a.K[(pod * H + h) * 9 + k];
+    __syncthreads();
+    const float inv_sqrt_d = 1.0f / __builtin_sqrtf((float)kD);
+    float gv[8], gi[8], gx[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) gv[j] = gi[j] = gx[j] = 0.f;
+#pragma unroll
+    for (int k = 0; k < 9; ++k) {
+        // r = q - offset_k: halo cell (cy + 1 - dy_k, cx + 1 - dx_k)
+        const int hc = (cy + 1 - (k / 3 - 1)) * kGHx + (cx + 1 - (k % 3 - 1));
+        const float ak = sA[hc * 9 + k], gs = sS[hc * 9 + k] * inv_sqrt_d;
+        const float4 v0 = *reinterpret_cast<const float4*>(sV + hc * kGRowF + c0);
+        const float4 v1 = *reinterpret_cast<const float4*>(sV + hc * kGRowF + c0 + 4);
+        const float4 p0 = *reinterpret_cast<const float4*>(sP + hc * kGRowF + c0);
+        const float4 p1 = *reinterpret_cast<const float4*>(sP + hc * kGRowF + c0 + 4);
+        const float4 u0 = *reinterpret_cast<const float4*>(sU + hc * kGRowF + c0);
+        const float4 u1 = *reinterpret_cast<const float4*>(sU + hc * kGRowF + c0 + 4);
+        const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+        const float pp[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+        const float uu[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            gv[j] = __builtin_fmaf(ak, vv[j], gv[j]);
+            gi[j] = __builtin_fmaf(gs, pp[j], gi[j]);
+            gx[j] = __builtin_fmaf(kw[k], uu[j], gx[j]);
+        }
+    }
+    const float ipv[8] = {ip0.v[0], ip0.v[1], ip0.v[2], ip0.v[3], ip1.v[0], ip1.v[1], ip1.v[2], ip1.v[3]};
+    const float gdv[8] = {gd0.v[0], gd0.v[1], gd0.v[2], gd0.v[3], gd1.v[0], gd1.v[1], gd1.v[2], gd1.v[3]};
+    float g1a[4], g1b[4], gva[4], gvb[4], gxa[4], gxb[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        g1a[j] = gi[j] * gelu_grad(ipv[j]);
+        g1b[j] = gi[j + 4] * gelu_grad(ipv[j + 4]);
+        gva[j] = gv[j];
+        gvb[j] = gv[j + 4];
+        gxa[j] = gdv[j] + gx[j];
+        gxb[j] = gdv[j + 4] + gx[j + 4];
+    }
+    const long long g3 = q * 3 * C + h * kD + c0;
+    st4<T>(a.G3, g3 + C, g1a);
+    st4<T>(a.G3, g3 + C + 4, g1b);
+    st4<T>(a.G3, g3 + 2 * C, gva);
+    st4<T>(a.G3, g3 + 2 * C + 4, gvb);
+    st4f(a.gXd, e0, gxa);
+    st4f(a.gXd, e0 + 4, gxb);
+}
+
 // ---- parameter finalize: fixed-order sums of the per-block partials ----------------------------
 __global__ __launch_bounds__(256) void bw_param_finalize_kernel(BackwardArgs a) {
     // one block per (pod, head, quantity): thread t adds partials t, t + 256, ... in
@@ -727,7 +830,11 @@ hipError_t launch_dt(const BackwardArgs& a, hipStream_t s) {
     hipLaunchKernelGGL((bw_loss_partial_kernel<T>), dim3(a.lchunks, a.B), dim3(256), 0, s, a);
     hipLaunchKernelGGL(bw_loss_finalize_kernel, dim3(a.B * kHeads), dim3(256), 0, s, a);
     hipLaunchKernelGGL((bw_cell_kernel<T, kD>), dim3(a.pods * a.nW), dim3(256), 0, s, a);
-    hipLaunchKernelGGL((bw_gather_kernel<T, kD>), dim3((unsigned)((n / 4 + 255) / 256)), dim3(256), 0, s, a);
+    if constexpr (kD == 64)
+        hipLaunchKernelGGL((bw_gather_tile_kernel<T>),
+                           dim3((unsigned)(a.B * (cells / (kGTy * kGTx)) * kHeads)), dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL((bw_gather_kernel<T, kD>), dim3((unsigned)((n / 4 + 255) / 256)), dim3(256), 0, s, a);
     hipLaunchKernelGGL(bw_param_finalize_kernel, dim3(a.pods * kHeads * kPartF), dim3(256), 0, s, a);
     if (a.per_cell)
         hipLaunchKernelGGL(bw_cell_param_finalize_kernel,
