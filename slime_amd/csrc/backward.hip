@@ -201,14 +201,19 @@ __global__ __launch_bounds__(256) void bw_cell_kernel(BackwardArgs a) {
     __shared__ __attribute__((aligned(16))) float sgy[kCpi * C];  // gY of the block's cells
     const int G = a.G;
     const long long cells = (long long)G * G;
-    const int w = blockIdx.x % a.nW;
     const int pod = blockIdx.x / a.nW;
     const int grp = threadIdx.x / kL, li = threadIdx.x % kL;
     const int cs = grp / H, h = grp % H;
     const int c0 = 4 * li;
-    // A multiple of kCpi (G is a multiple of 8), so every slot of an iteration is a cell
-    // and all threads of the block run the same iterations (they meet at barriers).
+    // A multiple of 8 kCpi (G is a multiple of 8), so every slot of an iteration is a
+    // cell and all threads of the block run the same iterations (they meet at barriers).
     const long long pod_cells = (long long)a.per_pod * cells;
+    // Workgroups are dealt to the 8 XCDs in turn (blockIdx % 8); XCD x walks the x-th
+    // eighth of the pod's cells, its workgroups on adjacent cell pairs, so a cell's
+    // neighbours (the next row included) are read from the L2 of the XCD that read
+    // them last.
+    const int nWx = a.nW / 8, wx = (blockIdx.x % a.nW) / 8, xcd = blockIdx.x % 8;
+    const long long band = pod_cells / 8;
     const float inv_sqrt_d = 1.0f / __builtin_sqrtf((float)kD);
     const float dt = a.dt;
     float mcol[H];
@@ -223,8 +228,8 @@ __global__ __launch_bounds__(256) void bw_cell_kernel(BackwardArgs a) {
 #pragma unroll
     for (int k = 0; k < 9; ++k) pK[k] = 0.f;
 
-    for (long long i0 = (long long)w * kCpi; i0 < pod_cells; i0 += (long long)a.nW * kCpi) {
-        const long long i = i0 + cs;
+    for (long long i0 = (long long)wx * kCpi; i0 < band; i0 += (long long)nWx * kCpi) {
+        const long long i = xcd * band + i0 + cs;
         const int b = pod * a.per_pod + (int)(i / cells);
         const long long cell = i % cells;
         const int y = (int)(cell / G), x = (int)(cell % G);
@@ -387,7 +392,7 @@ __global__ __launch_bounds__(256) void bw_cell_kernel(BackwardArgs a) {
         for (int c2 = 0; c2 < kCpi; ++c2)
 #pragma unroll
             for (int l2 = 0; l2 < kL; ++l2) sum += red[q][(c2 * H + hh) * kL + l2];
-        a.ppart[((long long)(pod * H + hh) * a.nW + w) * kPartF + q] = sum;
+        a.ppart[((long long)(pod * H + hh) * a.nW + blockIdx.x % a.nW) * kPartF + q] = sum;
     }
 }
 
