@@ -205,15 +205,19 @@ __global__ __launch_bounds__(256) void bw_cell_kernel(BackwardArgs a) {
     const int grp = threadIdx.x / kL, li = threadIdx.x % kL;
     const int cs = grp / H, h = grp % H;
     const int c0 = 4 * li;
-    // A multiple of 8 kCpi (G is a multiple of 8), so every slot of an iteration is a
-    // cell and all threads of the block run the same iterations (they meet at barriers).
+    // pod_cells is a multiple of kCpi (G is a multiple of 8, kCpi <= 16), so every slot
+    // of an iteration is a cell and all threads of the block run the same iterations
+    // (they meet at barriers).
     const long long pod_cells = (long long)a.per_pod * cells;
     // Workgroups are dealt to the 8 XCDs in turn (blockIdx % 8); XCD x walks the x-th
     // eighth of the pod's cells, its workgroups on adjacent cell pairs, so a cell's
     // neighbours (the next row included) are read from the L2 of the XCD that read
-    // them last.
-    const int nWx = a.nW / 8, wx = (blockIdx.x % a.nW) / 8, xcd = blockIdx.x % 8;
-    const long long band = pod_cells / 8;
+    // them last. When the eighths are not whole iterations (small grids), one band.
+    const bool banded = pod_cells % (8LL * kCpi) == 0;
+    const int nWx = banded ? a.nW / 8 : a.nW;
+    const int wx = banded ? (blockIdx.x % a.nW) / 8 : blockIdx.x % a.nW;
+    const int xcd = banded ? blockIdx.x % 8 : 0;
+    const long long band = banded ? pod_cells / 8 : pod_cells;
     const float inv_sqrt_d = 1.0f / __builtin_sqrtf((float)kD);
     const float dt = a.dt;
     float mcol[H];

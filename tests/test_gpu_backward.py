@@ -46,14 +46,17 @@ def _dev(a, dtype):
     return t.to(torch.bfloat16 if dtype == "bf16" else torch.float32).contiguous()
 
 
-@pytest.mark.parametrize("dtype,D,pods,per_cell", [
-    ("fp32", 16, 2, False),
-    ("fp32", 32, 1, True),
-    ("bf16", 64, 1, False),
-    ("bf16", 64, 2, True),
+@pytest.mark.parametrize("dtype,D,pods,per_cell,B,G", [
+    ("fp32", 16, 2, False, 2, 16),
+    ("fp32", 32, 1, True, 2, 16),
+    ("bf16", 64, 1, False, 2, 16),
+    ("bf16", 64, 2, True, 2, 16),
+    # the smallest grid: 64 cells per pod, fewer than 8 whole cell-pass iterations
+    ("fp32", 8, 1, False, 1, 8),
+    ("fp32", 8, 3, True, 3, 8),
 ])
-def test_backward_matches_oracle(oracle, dtype, D, pods, per_cell):
-    cfg = _cfg(B=2, G=16, D=D, dtype=dtype, pods=pods, growth_per_cell=per_cell)
+def test_backward_matches_oracle(oracle, dtype, D, pods, per_cell, B, G):
+    cfg = _cfg(B=B, G=G, D=D, dtype=dtype, pods=pods, growth_per_cell=per_cell)
     print(f"[case] backward {dtype} D={D} pods={pods} per_cell={per_cell}", flush=True)
     p, X, T = _inputs(cfg)
     with Pseudopod(cfg.B, cfg.G, cfg.H, cfg.D, cfg.dtype, cfg.dt, per_cell, pods) as e:
