@@ -733,12 +733,17 @@ int slime_ca_backward(slime_ca* h, const void* x_in, const void* target, float* 
         g.M = c.B * c.G * c.G;
         g.N = (int)C;
         g.K = (int)(3 * C);
-        g.out[0] = h->bw_gXp;
         g.ncol = (int)C;
         g.act[0] = 0;
-        HIP_TRY(launch_gemm(c.dtype, g, s));
+        if (gemm_uses_mfma(c.dtype, g)) {  // grad_x = gXd + the GEMM, from its epilogue
+            g.out[0] = grad_x;
+            HIP_TRY(launch_gemm_add_f32(c.dtype, g, h->bw_gXd, s));
+        } else {
+            g.out[0] = h->bw_gXp;
+            HIP_TRY(launch_gemm(c.dtype, g, s));
+            HIP_TRY(launch_backward_final(c.dtype, h->bw_gXd, h->bw_gXp, grad_x, (long long)n, s));
+        }
     }
-    HIP_TRY(launch_backward_final(c.dtype, h->bw_gXd, h->bw_gXp, grad_x, (long long)n, s));
     if (want_w) {
         DwArgs d{};
         d.part = h->bw_dwpart;

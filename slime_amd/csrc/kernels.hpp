@@ -24,6 +24,9 @@ struct GemmArgs {
 // kernel runs). dtype: 0 fp32, 1 bf16.
 bool gemm_uses_mfma(int dtype, const GemmArgs& a);
 hipError_t launch_gemm(int dtype, const GemmArgs& a, hipStream_t s);
+// One output plane (N = ncol, identity) written as fp32 out[0] = A Bt^T + add, add of
+// out[0]'s layout (in place allowed); MFMA shapes only (else hipErrorInvalidValue).
+hipError_t launch_gemm_add_f32(int dtype, const GemmArgs& a, const float* add, hipStream_t s);
 
 // ---- per-batch scaled, transposed weights -------------------------------------
 // Wt[b][p*C + n][k] = cvt( scale_p(b, k) * Wtm[pod(b)][p*C + n][k] ), where the
