@@ -22,6 +22,9 @@
 // leave as whole 128-byte row segments. Workgroups walk an XCD-contiguous tile
 // range, N fastest, so a cell block and one batch's weights are re-read from that
 // XCD's L2.
+// The tile kernel and its helpers are in gemm_tile.hpp (also built, with an adding
+// fp32 epilogue, by gemm_add.hip); this file holds the fallback, the launchers and
+// the weight folding.
 #include "gemm_tile.hpp"
 
 namespace slime {
