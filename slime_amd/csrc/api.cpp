@@ -140,6 +140,15 @@ int validate(const slime_ca_config* c) {
     if (c->pvi_chain != 0 && c->pvi_chain != 1) return fail(SLIME_EINVAL, "pvi_chain must be 0 or 1");
     const double elems = (double)c->B * c->G * c->G * c->H * c->D;
     if (elems > 4.0e9) return fail(SLIME_EINVAL, "state of %.3g elements is too large", elems);
+    // The stencils address one batch entry with 32-bit offsets: element offsets in
+    // int and byte offsets in unsigned, the bytes of the widest array they read or
+    // write (the fp32 output of a call's last step, also for a bf16 state).
+    const double per_batch = (double)c->G * c->G * c->H * c->D;
+    if (per_batch >= 2147483648.0 || per_batch * 4.0 >= 4294967296.0)
+        return fail(SLIME_EINVAL,
+                    "one batch entry of %.3g elements (G=%d, C=%d) exceeds the 32-bit per-batch "
+                    "offsets of the stencil (G*G*C*4 bytes must stay below 2^32)",
+                    per_batch, c->G, c->H * c->D);
     return SLIME_OK;
 }
 
@@ -407,6 +416,15 @@ int slime_ca_set_params(slime_ca* h, const slime_ca_params* p) {
         return fail(SLIME_EINVAL, "a parameter pointer is NULL");
     const slime_ca_config& c = h->cfg;
     const size_t C = h->C, CC = C * C;
+    // Every input is checked before the first upload, so a rejected call leaves the
+    // handle's parameters as they were.
+    const size_t ng = n_param_growth(c);
+    for (size_t i = 0; i < ng; ++i)
+        if (!std::isfinite(p->sigma[i]) || !std::isfinite(p->mu[i]))
+            return fail(SLIME_EINVAL, "mu/sigma entry %zu is not finite", i);
+    // From here a failed upload leaves a mix of old and new parameters: the handle
+    // refuses to step until a later call succeeds.
+    h->params_set = false;
     // Masters are kept transposed, [pods][p*C + n][k], so the per-step weight
     // preparation reads and writes along k.
     {
@@ -434,10 +452,6 @@ int slime_ca_set_params(slime_ca* h, const slime_ca_params* p) {
         (void)hipFree(h->Wcat);
         h->Wcat = nullptr;
     }
-    const size_t ng = n_param_growth(c);
-    for (size_t i = 0; i < ng; ++i)
-        if (!std::isfinite(p->sigma[i]) || !std::isfinite(p->mu[i]))
-            return fail(SLIME_EINVAL, "mu/sigma entry %zu is not finite", i);
     HIP_TRY(hipMemcpy(h->K, p->K, (size_t)c.pods * c.H * 9 * 4, hipMemcpyHostToDevice));
     if (h->kmat) {
         std::vector<uint16_t> km(stencil_kmat_bytes(c.pods) / 2);

@@ -49,13 +49,8 @@ __global__ __launch_bounds__(256) void gemm_simple_kernel(GemmArgs g) {
 template <typename T>
 hipError_t launch_t(const GemmArgs& a, hipStream_t s, bool mfma) {
     if (mfma) {
-        static int n_cu = 0;
-        if (!n_cu) {
-            int dev = 0;
-            hipError_t e = hipGetDevice(&dev);
-            if (e == hipSuccess) e = hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev);
-            if (e != hipSuccess) return e;
-        }
+        int n_cu = 0;
+        if (hipError_t e = device_cu_count(&n_cu); e != hipSuccess) return e;
         const int ntiles = (a.M / kBM) * (a.N / kBN);
         const int grid = ntiles < n_cu ? ntiles : n_cu;  // one persistent WG per CU
         hipLaunchKernelGGL(gemm_mfma_kernel<T>, dim3(grid), dim3(kThreads), 0, s, a);

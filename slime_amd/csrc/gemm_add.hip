@@ -9,13 +9,8 @@ namespace slime {
 
 hipError_t launch_gemm_add_f32(int dtype, const GemmArgs& a, const float* add, hipStream_t s) {
     if (!gemm_uses_mfma(dtype, a) || a.N != a.ncol || a.act[0] != 0 || !add) return hipErrorInvalidValue;
-    static int n_cu = 0;
-    if (!n_cu) {
-        int dev = 0;
-        hipError_t e = hipGetDevice(&dev);
-        if (e == hipSuccess) e = hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev);
-        if (e != hipSuccess) return e;
-    }
+    int n_cu = 0;
+    if (hipError_t e = device_cu_count(&n_cu); e != hipSuccess) return e;
     const int ntiles = (a.M / kBM) * (a.N / kBN);
     const int grid = ntiles < n_cu ? ntiles : n_cu;  // one persistent WG per CU
     if (dtype == 1)

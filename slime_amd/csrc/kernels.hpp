@@ -8,6 +8,10 @@ namespace slime {
 
 constexpr int kHeads = 8;  // NUM_HEADS, slime/core/pseudopod.cu:15
 
+// Compute units of the current device, queried once per device and cached (the
+// persistent kernels size their grids by it).
+hipError_t device_cu_count(int* n_cu);
+
 // ---- S1 projections ----------------------------------------------------------
 // out_p[m][col] = act_p( sum_k A[m][k] * Bt[batch(m)][n][k] ), n = p*ncol + col.
 struct GemmArgs {

@@ -10,10 +10,35 @@
 // The scale is not applied in a separate pass after every step: the next step
 // folds it into its weights (X_o W = X (diag(s) W)) and into its stencil loads,
 // and only the last step of a call is rescaled here, once.
+#include <atomic>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
 namespace slime {
+
+hipError_t device_cu_count(int* n_cu) {
+    constexpr int kMaxDevices = 64;
+    static std::atomic<int> cached[kMaxDevices] = {};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev >= 0 && dev < kMaxDevices) {
+        const int c = cached[dev].load(std::memory_order_relaxed);
+        if (c > 0) {
+            *n_cu = c;
+            return hipSuccess;
+        }
+    }
+    int n = 0;
+    e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return e;
+    if (n < 1) return hipErrorInvalidDevice;
+    if (dev >= 0 && dev < kMaxDevices) cached[dev].store(n, std::memory_order_relaxed);
+    *n_cu = n;
+    return hipSuccess;
+}
+
 namespace {
 
 __global__ __launch_bounds__(64) void mass_finalize_kernel(const float* part_in,

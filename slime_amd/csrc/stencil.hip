@@ -961,13 +961,8 @@ hipError_t launch_tdy(const StencilArgs& a, hipStream_t s) {
 
 template <typename TY>
 hipError_t launch_mfma(const StencilArgs& a, hipStream_t s) {
-    static int n_cu = 0;
-    if (!n_cu) {
-        int dev = 0;
-        hipError_t e = hipGetDevice(&dev);
-        if (e == hipSuccess) e = hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev);
-        if (e != hipSuccess) return e;
-    }
+    int n_cu = 0;
+    if (hipError_t e = device_cu_count(&n_cu); e != hipSuccess) return e;
     const int tiles = a.B * (a.G / kTileY) * (a.G / kTileX);
     const int grid = tiles < 2 * n_cu ? tiles : 2 * n_cu;  // two persistent workgroups per CU
     hipLaunchKernelGGL((stencil_mfma_kernel<TY>), dim3(grid), dim3(mf::kThreads), 0, s, a);

@@ -48,6 +48,36 @@ def test_create_rejects_invalid_config(bad):
     assert lib.slime_ca_last_error()
 
 
+@pytest.mark.parametrize("bad", [
+    # bf16: G*G*C = 2056^2 * 512 > 2^31, past the stencil's int element offsets
+    dict(B=1, G=2056, D=64, dtype=_lib.SLIME_BF16),
+    # fp32: G*G*C*4 = 1456^2 * 512 * 4 > 2^32, past its unsigned byte offsets
+    dict(B=1, G=1456, D=64, dtype=_lib.SLIME_F32),
+    # bf16 state whose last step is written in fp32: 1456^2 * 512 * 4 > 2^32 too
+    dict(B=1, G=1456, D=64, dtype=_lib.SLIME_BF16),
+])
+def test_create_rejects_batch_entries_past_32bit_offsets(bad):
+    """validate() runs before any device call, so this needs no GPU."""
+    lib = _lib.load()
+    h = ctypes.c_void_p()
+    rc = lib.slime_ca_create(ctypes.byref(_cfg(**bad)), ctypes.byref(h))
+    assert rc == _lib.SLIME_EINVAL
+    assert not h.value
+    assert b"32-bit" in lib.slime_ca_last_error()
+
+
+def test_largest_batch_entry_within_32bit_offsets_is_not_rejected_as_too_large():
+    """G = 1448 fp32 (1448^2 * 512 * 4 < 2^32) passes validation: without a GPU the
+    call fails later, at the device check, not with the offset message."""
+    lib = _lib.load()
+    h = ctypes.c_void_p()
+    rc = lib.slime_ca_create(ctypes.byref(_cfg(B=1, G=1448, D=64)), ctypes.byref(h))
+    if rc == _lib.SLIME_OK:  # a GPU is visible and had the memory
+        lib.slime_ca_destroy(h)
+        return
+    assert b"32-bit" not in lib.slime_ca_last_error()
+
+
 def test_null_arguments_are_errors_not_crashes():
     lib = _lib.load()
     assert lib.slime_ca_create(None, None) == _lib.SLIME_EINVAL
