@@ -42,10 +42,10 @@ struct slime_ca {
     void* V = nullptr;
     void* S[2] = {nullptr, nullptr};  // unscaled step outputs (ping-pong)
     float* Sf = nullptr;       // unscaled fp32 output of a call's last step (bf16 state only)
-    float* part_in = nullptr;  // [B*H][tiles]
-    float* part_out = nullptr;
-    float* scale[2] = {nullptr, nullptr};  // [B*H]
-    float* unit_scale = nullptr;           // [B*H] of 1.0
+    double* part_in = nullptr;  // [B*H][tiles]
+    double* part_out = nullptr;
+    float* scale[2] = {nullptr, nullptr};  // [2][B*H]: high parts, then low parts
+    float* unit_scale = nullptr;           // [2][B*H]: 1.0, then 0.0
     double* mass_in = nullptr;             // [B*H]
     double* mass_out = nullptr;
 
@@ -372,11 +372,12 @@ int slime_ca_create(const slime_ca_config* config, slime_ca** out) {
     rc = rc ? rc : dalloc(&h->S[0], state_bytes);
     rc = rc ? rc : dalloc(&h->S[1], state_bytes);
     if (c.dtype == SLIME_BF16) rc = rc ? rc : dalloc_t(&h->Sf, (size_t)h->state_elems * 4);
-    rc = rc ? rc : dalloc_t(&h->part_in, BH * h->tiles * 4);
-    rc = rc ? rc : dalloc_t(&h->part_out, BH * h->tiles * 4);
-    rc = rc ? rc : dalloc_t(&h->scale[0], BH * 4);
-    rc = rc ? rc : dalloc_t(&h->scale[1], BH * 4);
-    rc = rc ? rc : dalloc_t(&h->unit_scale, BH * 4);
+    rc = rc ? rc : dalloc_t(&h->part_in, BH * h->tiles * 8);
+    rc = rc ? rc : dalloc_t(&h->part_out, BH * h->tiles * 8);
+    // scales: [2][B*H] fp32, the high parts then the low parts (scale = hi + lo)
+    rc = rc ? rc : dalloc_t(&h->scale[0], 2 * BH * 4);
+    rc = rc ? rc : dalloc_t(&h->scale[1], 2 * BH * 4);
+    rc = rc ? rc : dalloc_t(&h->unit_scale, 2 * BH * 4);
     rc = rc ? rc : dalloc_t(&h->mass_in, BH * 8);
     rc = rc ? rc : dalloc_t(&h->mass_out, BH * 8);
     rc = rc ? rc : dalloc_t(&h->sweeps, BH * sizeof(int));
@@ -385,9 +386,9 @@ int slime_ca_create(const slime_ca_config* config, slime_ca** out) {
         delete h;
         return rc;
     }
-    float* ones = new float[BH];
-    for (size_t i = 0; i < BH; ++i) ones[i] = 1.0f;
-    hipError_t e = hipMemcpy(h->unit_scale, ones, BH * 4, hipMemcpyHostToDevice);
+    float* ones = new float[2 * BH];
+    for (size_t i = 0; i < 2 * BH; ++i) ones[i] = i < BH ? 1.0f : 0.0f;
+    hipError_t e = hipMemcpy(h->unit_scale, ones, 2 * BH * 4, hipMemcpyHostToDevice);
     delete[] ones;
     if (e == hipSuccess) e = hipMemset(h->mass_in, 0, BH * 8);
     if (e == hipSuccess) e = hipMemset(h->mass_out, 0, BH * 8);

@@ -47,7 +47,8 @@ hipError_t launch_weight_prep(int dtype, const WeightPrepArgs& a, hipStream_t s)
 // ---- S2-S6 fused stencil --------------------------------------------------------
 struct StencilArgs {
     const void* X;           // [B][G][G][C] state (stored, before scale)
-    const float* scale_in;   // [B][H] deferred mass scale for X (nullptr = 1)
+    const float* scale_in;   // [2][B][H] deferred mass scale for X, high then low parts
+                             // (scale = hi + lo to ~2^-48); nullptr = 1
     const void* P;
     const void* I;
     const void* V;
@@ -61,8 +62,8 @@ struct StencilArgs {
     // matrices over a 4x8 tile's 6x10 halo, [pods][H][2][32 cells][64 halo rows]
     // (stencil_kmat_bytes / fill_stencil_kmat).
     const void* kmat;
-    float* part_in;          // [B][H][tiles]  sum of scaled X per tile
-    float* part_out;         // [B][H][tiles]  sum of stored Y per tile
+    double* part_in;         // [B][H][tiles]  sum of scaled X per tile
+    double* part_out;        // [B][H][tiles]  sum of stored Y per tile
     int B, G, D, per_pod, per_cell;
     float dt;
 };
@@ -74,12 +75,16 @@ void fill_stencil_kmat(const float* K, int pods, uint16_t* out);
 hipError_t launch_stencil(int dtype, const StencilArgs& a, hipStream_t s);
 
 // ---- S7 mass conservation ------------------------------------------------------------
-// scale[b][h] = |sum_out| > 1e-6 ? sum_in / sum_out : 1, reduced in fixed order.
-hipError_t launch_mass_finalize(const float* part_in, const float* part_out, int BH, int tiles,
+// scale[b][h] = |sum_out| > 1e-6 ? sum_in / sum_out : 1, reduced in fixed order,
+// written as two floats per (b, h): scale_out[0][b][h] the fp32 rounding of the
+// fp64 ratio, scale_out[1][b][h] the fp32 rounding of the rest. A scale applied
+// as x * hi + x * lo carries no rounding bias from step to step, so the mass of a
+// long chain of steps does not drift with the rounding of the ratio.
+hipError_t launch_mass_finalize(const double* part_in, const double* part_out, int BH, int tiles,
                                 double* mass_in, double* mass_out, float* scale_out,
                                 hipStream_t s);
-// y[i] = cvt(scale[b][h] * x[i]) over the whole state; x is fp32 when x_f32 is
-// set, else in the storage type.
+// y[i] = cvt((scale[0][b][h] + scale[1][b][h]) * x[i]) over the whole state; x is
+// fp32 when x_f32 is set, else in the storage type.
 hipError_t launch_rescale(int dtype, const void* x, int x_f32, const float* scale, void* y, int B,
                           int G, int C, int D, hipStream_t s);
 

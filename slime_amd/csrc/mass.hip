@@ -41,8 +41,8 @@ hipError_t device_cu_count(int* n_cu) {
 
 namespace {
 
-__global__ __launch_bounds__(64) void mass_finalize_kernel(const float* part_in,
-                                                           const float* part_out, int tiles,
+__global__ __launch_bounds__(64) void mass_finalize_kernel(const double* part_in,
+                                                           const double* part_out, int tiles,
                                                            double* mass_in, double* mass_out,
                                                            float* scale_out) {
     // One wave per (b, h): lanes stride over tiles, then a fixed-shape tree.
@@ -50,8 +50,8 @@ __global__ __launch_bounds__(64) void mass_finalize_kernel(const float* part_in,
     const int bh = blockIdx.x, lane = threadIdx.x;
     double si = 0.0, so = 0.0;
     for (int t = lane; t < tiles; t += 64) {
-        si += (double)part_in[(long long)bh * tiles + t];
-        so += (double)part_out[(long long)bh * tiles + t];
+        si += part_in[(long long)bh * tiles + t];
+        so += part_out[(long long)bh * tiles + t];
     }
     s_in[lane] = si;
     s_out[lane] = so;
@@ -65,17 +65,19 @@ __global__ __launch_bounds__(64) void mass_finalize_kernel(const float* part_in,
     }
     if (lane == 0) {
         const double in = s_in[0], out = s_out[0];
-        const float scale = fabs(out) > 1e-6 ? (float)(in / out) : 1.0f;
-        scale_out[bh] = scale;
+        const double r = fabs(out) > 1e-6 ? in / out : 1.0;
+        const float hi = (float)r, lo = (float)(r - (double)hi);
+        scale_out[bh] = hi;
+        scale_out[gridDim.x + bh] = lo;
         mass_in[bh] = in;
-        mass_out[bh] = (double)scale * out;
+        mass_out[bh] = ((double)hi + (double)lo) * out;
     }
 }
 
 template <typename TI, typename T>
 __global__ __launch_bounds__(256) void rescale_kernel(const TI* x, const float* scale, T* y,
                                                       long long nquads, int C, int D,
-                                                      long long cells_per_batch) {
+                                                      long long cells_per_batch, int bh_total) {
     // Four consecutive elements per thread; they never straddle two heads (D >= 8).
     const long long q = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (q >= nquads) return;
@@ -83,7 +85,8 @@ __global__ __launch_bounds__(256) void rescale_kernel(const TI* x, const float* 
     const long long cell = e0 / C;
     const int ch = (int)(e0 - cell * C);
     const int b = (int)(cell / cells_per_batch);
-    const float s = scale[b * (C / D) + ch / D];
+    const long long si = (long long)b * (C / D) + ch / D;
+    const float s = scale[si], s_lo = scale[bh_total + si];
     float v[4];
     if constexpr (sizeof(TI) == 2) {
         const uint2 w = reinterpret_cast<const uint2*>(x)[q];
@@ -92,17 +95,18 @@ __global__ __launch_bounds__(256) void rescale_kernel(const TI* x, const float* 
         const float4 f = reinterpret_cast<const float4*>(x)[q];
         v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
     }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = __builtin_fmaf(v[i], s_lo, v[i] * s);
     if constexpr (sizeof(T) == 2) {
-        reinterpret_cast<uint2*>(y)[q] =
-            make_uint2(pack_bf16x2(v[0] * s, v[1] * s), pack_bf16x2(v[2] * s, v[3] * s));
+        reinterpret_cast<uint2*>(y)[q] = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
     } else {
-        reinterpret_cast<float4*>(y)[q] = make_float4(v[0] * s, v[1] * s, v[2] * s, v[3] * s);
+        reinterpret_cast<float4*>(y)[q] = make_float4(v[0], v[1], v[2], v[3]);
     }
 }
 
 }  // namespace
 
-hipError_t launch_mass_finalize(const float* part_in, const float* part_out, int BH, int tiles,
+hipError_t launch_mass_finalize(const double* part_in, const double* part_out, int BH, int tiles,
                                 double* mass_in, double* mass_out, float* scale_out,
                                 hipStream_t s) {
     hipLaunchKernelGGL(mass_finalize_kernel, dim3(BH), dim3(64), 0, s, part_in, part_out, tiles,
@@ -115,18 +119,19 @@ hipError_t launch_rescale(int dtype, const void* x, int x_f32, const float* scal
     const long long cells = (long long)G * G;
     const long long nquads = (long long)B * cells * C / 4;
     const dim3 grid((unsigned)((nquads + 255) / 256));
+    const int bh = B * (C / D);
     if (dtype == 1 && x_f32)
         hipLaunchKernelGGL((rescale_kernel<float, bf16_t>), grid, dim3(256), 0, s,
                            static_cast<const float*>(x), scale, static_cast<bf16_t*>(y), nquads, C,
-                           D, cells);
+                           D, cells, bh);
     else if (dtype == 1)
         hipLaunchKernelGGL((rescale_kernel<bf16_t, bf16_t>), grid, dim3(256), 0, s,
                            static_cast<const bf16_t*>(x), scale, static_cast<bf16_t*>(y), nquads, C,
-                           D, cells);
+                           D, cells, bh);
     else
         hipLaunchKernelGGL((rescale_kernel<float, float>), grid, dim3(256), 0, s,
                            static_cast<const float*>(x), scale, static_cast<float*>(y), nquads, C,
-                           D, cells);
+                           D, cells, bh);
     return hipGetLastError();
 }
 

@@ -176,7 +176,7 @@ __global__ __launch_bounds__((Layout<T, D>::kThreads), 2) void stencil_kernel(St
     __shared__ __attribute__((aligned(16))) unsigned char bufB[L::kBufB];
     __shared__ __attribute__((aligned(16))) float sAtt[2][kTileCells * kAStride];
     __shared__ __attribute__((aligned(16))) float sMS[H * kTileCells * 2];
-    __shared__ float sR[L::kWaves * 16];
+    __shared__ double sR[L::kWaves * 16];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -249,7 +249,7 @@ __global__ __launch_bounds__((Layout<T, D>::kThreads), 2) void stencil_kernel(St
     // Per-head parameters (and per-cell growth parameters) go to LDS once, before
     // any direct load is issued: reading them later from global memory would make
     // the in-order vector-memory counter wait for the next head's staging.
-    __shared__ float sK[H * 9], sMW[H * H], sGa[H], sGb[H], sScale[H];
+    __shared__ float sK[H * 9], sMW[H * H], sGa[H], sGb[H], sScale[H], sScaleLo[H];
     {
         constexpr float kLog2eP = 1.4426950408889634f;
         for (int i = tid; i < H * 9; i += L::kThreads) sK[i] = a.K[pod * H * 9 + i];
@@ -259,6 +259,7 @@ __global__ __launch_bounds__((Layout<T, D>::kThreads), 2) void stencil_kernel(St
         }
         if (tid < H) {
             sScale[tid] = a.scale_in ? a.scale_in[b * H + tid] : 1.0f;
+            sScaleLo[tid] = a.scale_in ? a.scale_in[a.B * H + b * H + tid] : 0.0f;
             if (!a.per_cell) {
                 const float ga = __builtin_sqrtf(kLog2eP) / (a.sigma[pod * H + tid] + 1e-7f);
                 sGa[tid] = ga;
@@ -349,7 +350,7 @@ __global__ __launch_bounds__((Layout<T, D>::kThreads), 2) void stencil_kernel(St
         // ---- phase B: potential, growth, propagation, update, head mixing --------------
         float xacc = 0.f;
         if (active) {
-            const float s_in = sScale[h];
+            const float s_in = sScale[h], s_lo = sScaleLo[h];
             float kw[9];
 #pragma unroll
             for (int k = 0; k < 9; ++k) kw[k] = sK[h * 9 + k];
@@ -407,7 +408,8 @@ __global__ __launch_bounds__((Layout<T, D>::kThreads), 2) void stencil_kernel(St
                     const float tg = __builtin_fmaf(u * s_in, ga, -gb);
                     const float ex = exp2_fast(-tg * tg);
                     const float coef = __builtin_fmaf(ex, two_dt, -dt);  // dt * g
-                    const float xc = (e ? xw[1][1].y : xw[1][1].x) * s_in;
+                    const float xv = e ? xw[1][1].y : xw[1][1].x;
+                    const float xc = __builtin_fmaf(xv, s_lo, xv * s_in);
                     z[e] = __builtin_fmaf(coef, vt, xc);
                     xacc += xc;
                 }
@@ -455,10 +457,12 @@ __global__ __launch_bounds__((Layout<T, D>::kThreads), 2) void stencil_kernel(St
             }
         }
     }
+    // Each lane's few values are summed in fp32; lanes, waves and tiles add in fp64,
+    // so the sums stay accurate when the state's values are large and of both signs.
 #pragma unroll
     for (int j = 0; j < H; ++j) {
-        const float sx = wave_sum(xin[j]);
-        const float sy = wave_sum(ysum[j]);
+        const double sx = wave_sum64(xin[j]);
+        const double sy = wave_sum64(ysum[j]);
         if (lane == 0) {
             sR[wave * 16 + j] = sx;
             sR[wave * 16 + H + j] = sy;
@@ -466,10 +470,10 @@ __global__ __launch_bounds__((Layout<T, D>::kThreads), 2) void stencil_kernel(St
     }
     __syncthreads();
     if (tid < 2 * H) {
-        float sum = 0.f;
+        double sum = 0.0;
         for (int w = 0; w < L::kWaves; ++w) sum += sR[w * 16 + tid];
         const int j = tid % H;
-        float* dst = tid < H ? a.part_in : a.part_out;
+        double* dst = tid < H ? a.part_in : a.part_out;
         dst[((long long)b * H + j) * tpb + tile] = sum;
     }
 }
@@ -515,9 +519,9 @@ constexpr int kAttB = kWC * kRowB;                          // one 16 x 64 bf16 
 constexpr int kS9 = 12;  // floats per cell in a score buffer (9 used, 9..11 take discards)
 constexpr int kKmatHead = 2 * kTileCells * kRowB;           // hi + lo, 8 KiB per (pod, head)
 // Per-tile parameter block (fp32): M[8][8] (M[o][h] at o*8+h), mu[8], sigma[8],
-// scale[8]; then, for per-cell growth, mu and sigma [cell][8].
-constexpr int kPM = 0, kPMu = 64, kPSg = 72, kPSc = 80, kPScal = 88;
-constexpr int kPCellMu = 88, kPCellSg = 88 + kTileCells * 8, kParF = 88 + 2 * kTileCells * 8;
+// scale[8] and its low part[8]; then, for per-cell growth, mu and sigma [cell][8].
+constexpr int kPM = 0, kPMu = 64, kPSg = 72, kPSc = 80, kPScLo = 88, kPScal = 96;
+constexpr int kPCellMu = 96, kPCellSg = 96 + kTileCells * 8, kParF = 96 + 2 * kTileCells * 8;
 
 // 16-byte chunk swizzles inside a 128-byte row. X and V: any four consecutive
 // rows 4j..4j+3, and rows {r, r+2, r+8, r+10}, occupy disjoint chunk pairs, so
@@ -553,13 +557,13 @@ __device__ __forceinline__ void split_bf16(float v, bf16_t& hi, bf16_t& lo) {
 // lane's copy (DPP kCtrl, whose partner differs from the lane in that bit and in
 // no bit a previous step used).
 template <int kN, int kCtrl>
-__device__ __forceinline__ void fold_half(float (&v)[16], int lane, int bit) {
+__device__ __forceinline__ void fold_half(double (&v)[16], int lane, int bit) {
     const bool up = (lane >> bit) & 1;
 #pragma unroll
     for (int i = 0; i < kN; ++i) {
-        const float keep = up ? v[i + kN] : v[i];
-        const float send = up ? v[i] : v[i + kN];
-        v[i] = keep + dpp_f32<kCtrl>(send);
+        const double keep = up ? v[i + kN] : v[i];
+        const double send = up ? v[i] : v[i + kN];
+        v[i] = keep + dpp_f64<kCtrl>(send);
     }
 }
 
@@ -584,7 +588,7 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
     // One parameter block: a tile's block is written after the barrier that ends
     // the previous tile's last head, its last reader.
     __shared__ __attribute__((aligned(16))) float sPar[kParF];
-    __shared__ float sR[kThreads];
+    __shared__ double sR[kThreads];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -673,8 +677,10 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
         if (tid < kPM + 64) pre[0] = a.M[pod * 64 + tid - kPM];
         else if (tid < kPSg + 8) {
             if (!a.per_cell) pre[0] = tid < kPSg ? a.mu[pod * 8 + tid - kPMu] : a.sigma[pod * 8 + tid - kPSg];
-        } else if (tid < kPScal) {
+        } else if (tid < kPScLo) {
             pre[0] = a.scale_in ? a.scale_in[b * 8 + tid - kPSc] : 1.0f;
+        } else if (tid < kPScal) {
+            pre[0] = a.scale_in ? a.scale_in[a.B * 8 + b * 8 + tid - kPScLo] : 0.0f;
         }
         if (a.per_cell) {
             const int ty0 = (tile / tiles_x) * kTileY, tx0 = (tile % tiles_x) * kTileX;
@@ -868,7 +874,8 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
                         }
                     }
                 }
-                const float s_in = par[kPSc + h];  // deferred mass scale of X
+                const float s_in = par[kPSc + h];  // deferred mass scale of X (high part)
+                const float s_lo = par[kPScLo + h];
                 const float two_dt = 2.0f * dt;
                 float mw[H];
 #pragma unroll
@@ -888,7 +895,7 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
                         const float tg = __builtin_fmaf(u[mb][e], ga, -gb);
                         const float ex = exp2_fast(-tg * tg);
                         const float coef = __builtin_fmaf(ex, two_dt, -dt);  // dt * g
-                        const float xc = xv[e] * s_in;
+                        const float xc = __builtin_fmaf(xv[e], s_lo, xv[e] * s_in);
                         const float z = __builtin_fmaf(coef, vt[mb][e], xc);
                         xacc += xc;
 #pragma unroll
@@ -902,12 +909,9 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
 
         // ---- store Y and the tile's mass partial sums -----------------------------------
         TY* Yg = static_cast<TY*>(a.Y);
-        float red[16];  // [0, 8): sum of scaled X per head; [8, 16): sum of stored Y
+        float ysum[H];  // this lane's sum of stored Y per head
 #pragma unroll
-        for (int o = 0; o < H; ++o) {
-            red[o] = xin[o];
-            red[H + o] = 0.f;
-        }
+        for (int o = 0; o < H; ++o) ysum[o] = 0.f;
         {
             const long long base =
                 bbase + ((long long)(ty0 + cell / kTileX) * G + tx0 + cell % kTileX) * C + ch0;
@@ -919,7 +923,7 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         r[e] = Store<TY>::round(y[o][mb][e]);
-                        red[H + o] += r[e];
+                        ysum[o] += r[e];
                     }
                     TY* dst = Yg + base + o * kD + 16 * mb;
                     // 32-byte pieces per cell: plain stores, so L2 merges the pieces of
@@ -932,6 +936,14 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
         }
         // Wave sums of the 16 values: the butterfly leaves lane l holding its 16-lane
         // row's sum of value l & 15; the rows and waves are added in a fixed order.
+        // Each lane's 8 values per head are summed in fp32, everything above in fp64,
+        // so the sums stay accurate when the state's values are large and of both signs.
+        double red[16];  // [0, 8): sum of scaled X per head; [8, 16): sum of stored Y
+#pragma unroll
+        for (int o = 0; o < H; ++o) {
+            red[o] = xin[o];
+            red[H + o] = ysum[o];
+        }
         fold_half<8, 0x140>(red, lane, 3);  // row_mirror: partner l ^ 15
         fold_half<4, 0x141>(red, lane, 2);  // row_half_mirror: partner l ^ 7
         fold_half<2, 0x4E>(red, lane, 1);   // quad_perm [2,3,0,1]: partner l ^ 2
@@ -939,11 +951,11 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
         sR[tid] = red[0];
         __syncthreads();
         if (tid < 2 * H) {
-            float sum = 0.f;
+            double sum = 0.0;
 #pragma unroll
             for (int r = 0; r < kThreads / 16; ++r) sum += sR[r * 16 + tid];
             const int j = tid % H;
-            float* dst = tid < H ? a.part_in : a.part_out;
+            double* dst = tid < H ? a.part_in : a.part_out;
             dst[((long long)b * H + j) * tpb + tile] = sum;
         }
         if (t_next < 0) break;
