@@ -8,24 +8,20 @@
 #include <type_traits>
 
 #include "common.hpp"
+#include "gemm_addr.hpp"
 #include "kernels.hpp"
 
 namespace slime {
 namespace {
 
-
-constexpr int kBM = 256, kBN = 256, kThreads = 256;
-constexpr int kSlabB = 64;                    // bytes of K per tile row per slab
-constexpr int kStageB = (kBM + kBN) * kSlabB;  // 32 KiB
-constexpr int kDmaPerSlab = 8;                // direct-load instructions per wave per slab
-
+// Tile shape, ring and staging constants, and all address arithmetic: gemm_addr.hpp.
 // Stage layout: tile row r (0..255 cells, 256..511 output channels) holds its 64
 // slab bytes at r*64, as four 16-byte chunks XOR-permuted by
 // f(r) = ((r >> 1) ^ (r >> 3)) & 3: physical chunk = logical chunk ^ f(r). One
 // direct-load instruction fills 16 whole rows (1 KiB, four lanes per 64-byte row),
 // and the operand reads -- 32 consecutive rows at one logical chunk per half
 // wave -- spread over the LDS banks.
-__device__ __forceinline__ constexpr int row_swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+using namespace gemm_addr;
 
 __device__ __forceinline__ float apply_act(float v, int act) {
     if (act == 1) return v > 0.f ? v : 0.f;
@@ -50,19 +46,17 @@ template <int kAct>
 __device__ __forceinline__ void store_tile_f32(f32x16 (&acc)[4][4], float* obase, int ncol) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        float* orow = obase + (long long)j * 32 * ncol;
 #pragma unroll
         for (int i = 0; i < 4; ++i) pin_acc(acc[i][j]);
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int q = 0; q < 4; ++q)
-                *reinterpret_cast<float4*>(orow + i * 32 + 8 * q) =
+                *reinterpret_cast<float4*>(obase + f32_store_elem(j, i, q, ncol)) =
                     make_float4(act_of<kAct>(acc[i][j][4 * q + 0]), act_of<kAct>(acc[i][j][4 * q + 1]),
                                 act_of<kAct>(acc[i][j][4 * q + 2]), act_of<kAct>(acc[i][j][4 * q + 3]));
     }
 }
-constexpr int kStoresF32 = 64;  // global stores per wave per tile (fp32 epilogue)
 
 #ifdef SLIME_GEMM_ADD
 // fp32 epilogue with an addend of the output's layout: out = acc + add (in place
@@ -71,31 +65,26 @@ __device__ __forceinline__ void store_tile_f32_add(f32x16 (&acc)[4][4], float* o
                                                    int ncol) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        float* orow = obase + (long long)j * 32 * ncol;
-        const float* arow = abase + (long long)j * 32 * ncol;
         float4 ad[4][4];
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int q = 0; q < 4; ++q) ad[i][q] = *reinterpret_cast<const float4*>(arow + i * 32 + 8 * q);
+            for (int q = 0; q < 4; ++q) ad[i][q] = *reinterpret_cast<const float4*>(abase + f32_store_elem(j, i, q, ncol));
 #pragma unroll
         for (int i = 0; i < 4; ++i) pin_acc(acc[i][j]);
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int q = 0; q < 4; ++q)
-                *reinterpret_cast<float4*>(orow + i * 32 + 8 * q) =
+                *reinterpret_cast<float4*>(obase + f32_store_elem(j, i, q, ncol)) =
                     make_float4(acc[i][j][4 * q + 0] + ad[i][q].x, acc[i][j][4 * q + 1] + ad[i][q].y,
                                 acc[i][j][4 * q + 2] + ad[i][q].z, acc[i][j][4 * q + 3] + ad[i][q].w);
     }
 }
 #endif
 
-// Rows of the per-wave staging region are padded to 144 bytes: the 8-byte writes
-// of 16 consecutive rows hit distinct banks.
-constexpr int kEpiRowB = 144;
-constexpr int kEpiWaveB = 32 * kEpiRowB;
-constexpr int kStoresBf16 = 32;  // global stores per wave per tile (bf16 epilogue)
+// Rows of the per-wave staging region are padded to 144 bytes (kEpiRowB): the
+// 8-byte writes of 16 consecutive rows hit distinct banks.
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
@@ -126,17 +115,11 @@ __device__ __forceinline__ unsigned lds_addr(const void* p) {
 // (row lane/4 of the group, the logical chunk that lands in physical chunk lane%4).
 __device__ __forceinline__ void issue_slab(const char* x, const char* w, long long row_bytes, int ks,
                                            int wave, unsigned voff, unsigned sbase) {
-    const long long k_off = (long long)ks * kSlabB;
+    const long long k_off = dma_k_off(ks);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int grp = 4 * j + wave;
-        dma16(x + grp * 16 * row_bytes + k_off, voff, sbase + grp * 1024);
-    }
+    for (int j = 0; j < 4; ++j) dma16(x + dma_grp_off(j, wave, row_bytes) + k_off, voff, sbase + dma_lds_off(j, wave));
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int grp = 4 * j + wave;
-        dma16(w + grp * 16 * row_bytes + k_off, voff, sbase + (16 + grp) * 1024);
-    }
+    for (int j = 4; j < 8; ++j) dma16(w + dma_grp_off(j, wave, row_bytes) + k_off, voff, sbase + dma_lds_off(j, wave));
 }
 
 // s_waitcnt vmcnt(n) for the counts the pipeline needs (immediate operand).
@@ -195,9 +178,9 @@ template <int R>
 __device__ __forceinline__ void read_frag(Frags& f, const unsigned char* stage, const FragBase& b) {
     constexpr int kk = R >> 3, q = R & 7;
     if constexpr (q < 4)
-        f.x[kk][q] = *reinterpret_cast<const u32x4*>(stage + b.x[kk] + q * 32 * kSlabB);
+        f.x[kk][q] = *reinterpret_cast<const u32x4*>(stage + b.x[kk] + frag_block_off(q));
     else
-        f.w[kk][q - 4] = *reinterpret_cast<const u32x4*>(stage + b.w[kk] + (q - 4) * 32 * kSlabB);
+        f.w[kk][q - 4] = *reinterpret_cast<const u32x4*>(stage + b.w[kk] + frag_block_off(q - 4));
 }
 
 // MFMA group M (0..31) of a slab: output block (i, j) = ((M / 4) % 4, M % 4) over
@@ -235,11 +218,10 @@ struct Walk {
 template <typename T>
 __device__ __forceinline__ void tile_rows(const GemmArgs& g, int tile, int nN, const char** x,
                                           const char** w) {
-    const int m0 = (tile / nN) * kBM, n0 = (tile % nN) * kBN;
-    const long long K = g.K;
-    *x = reinterpret_cast<const char*>(static_cast<const T*>(g.A) + m0 * K);
-    *w = reinterpret_cast<const char*>(static_cast<const T*>(g.Bt) +
-                                       (long long)(m0 / g.rows_per_batch) * g.bt_batch_stride + n0 * K);
+    long long xe, we;
+    tile_row_elems(tile, nN, g.K, g.rows_per_batch, g.bt_batch_stride, &xe, &we);
+    *x = reinterpret_cast<const char*>(static_cast<const T*>(g.A) + xe);
+    *w = reinterpret_cast<const char*>(static_cast<const T*>(g.Bt) + we);
 }
 
 // Scheduling-group masks (LLVM AMDGPU IGroupLP): MFMA and LDS-read instructions.
@@ -350,10 +332,9 @@ __device__ __forceinline__ void stage_read(const unsigned char* rp, uint4 (&tmp)
 }
 template <int Gr>
 __device__ __forceinline__ void store_group(char* ob, unsigned gl, int ncol, const uint4 (&tmp)[4]) {
-    constexpr int j = Gr >> 1, p = Gr & 1;
 #pragma unroll
     for (int s4 = 0; s4 < 4; ++s4) {
-        const long long uoff = ((long long)(j * 32 + s4 * 8) * ncol + p * 64) * 2;  // uniform
+        const long long uoff = bf16_store_off(Gr, s4, ncol);  // uniform
         __builtin_nontemporal_store(__builtin_bit_cast(u32x4, tmp[s4]),
                                     reinterpret_cast<u32x4*>(ob + uoff + gl));
     }
@@ -398,40 +379,24 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_add_kernel(GemmArgs g, 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar LDS addresses
-    const int wm = wave & 1, wn = wave >> 1;
-    const int r32 = lane & 31, half = lane >> 5;
 
     Walk wk;
     wk.nN = g.N / kBN;
     wk.nk = g.K / kSlabE;  // slabs per tile, a multiple of 4
     wk.row_bytes = (long long)g.K * (long long)sizeof(T);
-    // Direct loads: lane l fills physical chunk l%4 of row l/4 of a 16-row group whose
-    // first row is a multiple of 32 for even waves and 16 more for odd ones.
-    const int dma_row = lane >> 2;
-    const int dma_chunk = (lane & 3) ^ row_swz(16 * (wave & 1) + dma_row);
-    wk.voff = (unsigned)(dma_row * wk.row_bytes + dma_chunk * 16);
+    wk.voff = dma_lane_off(wave, lane, wk.row_bytes);
     const int ntiles = (g.M / kBM) * wk.nN;
-    if ((gridDim.x & 7) == 0) {
-        const int per_xcd_wg = gridDim.x >> 3;
-        const int xcd = blockIdx.x & 7, j = blockIdx.x >> 3;
-        const int span = (ntiles + 7) >> 3;
-        const int begin = xcd * span;
-        wk.tile_end = min(ntiles, begin + span);
-        wk.tile = begin + j;
-        wk.stride = per_xcd_wg;
-    } else {
-        wk.tile = blockIdx.x;
-        wk.stride = gridDim.x;
-        wk.tile_end = ntiles;
-    }
+    const Sched sc = schedule(blockIdx.x, gridDim.x, ntiles);
+    wk.tile = sc.tile;
+    wk.stride = sc.stride;
+    wk.tile_end = sc.tile_end;
     if (wk.tile >= wk.tile_end) return;
 
     FragBase fbase;
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
-        const unsigned lane_part = r32 * kSlabB + (((2 * kk + half) ^ row_swz(r32)) << 4);
-        fbase.x[kk] = lane_part + (wm * 128) * kSlabB;
-        fbase.w[kk] = lane_part + (kBM + wn * 128) * kSlabB;
+        fbase.x[kk] = frag_x_off(kk, lane, wave);
+        fbase.w[kk] = frag_w_off(kk, lane, wave);
     }
 
     // Prologue: slabs 0..3 of the first tile, then slab 0's fragments.
@@ -446,9 +411,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_add_kernel(GemmArgs g, 
 
     bool stores_pending = false;  // the previous tile's stores follow slabs 0..3 of this one
     f32x16 acc[4][4];
-    unsigned char* ep_w = epi + wave * kEpiWaveB + r32 * kEpiRowB + half * 8;
-    const unsigned char* ep_r = epi + wave * kEpiWaveB + (lane >> 3) * kEpiRowB + (lane & 7) * 16;
-    const unsigned ep_gl = (unsigned)(((lane >> 3) * g.ncol + (lane & 7) * 8) * 2);
+    unsigned char* ep_w = epi + epi_w_off(wave, lane);
+    const unsigned char* ep_r = epi + epi_r_off(wave, lane);
+    const unsigned ep_gl = epi_gl_off(lane, g.ncol);
     while (true) {
         wk.next = wk.tile + wk.stride < wk.tile_end ? wk.tile + wk.stride : -1;
         if (wk.next >= 0) tile_rows<T>(g, wk.next, wk.nN, &wk.x_nxt, &wk.w_nxt);
@@ -467,20 +432,18 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_add_kernel(GemmArgs g, 
         }
         // Slab 0 of the next tile is in stage 0 (published by the last step's barrier);
         // its fragments are read after the epilogue.
-        const int m0 = (wk.tile / wk.nN) * kBM, n0 = (wk.tile % wk.nN) * kBN;
-        const int plane = n0 / g.ncol;
+        const int plane = tile_plane(wk.tile, wk.nN, g.ncol);
         T* out = static_cast<T*>(g.out[plane]);
-        const int col0 = n0 - plane * g.ncol + wn * 128;
+        const long long wave_el = wave_out_elem(wk.tile, wk.nN, g.ncol, wave);
         // The whole 256-wide N tile lies in one output plane: uniform activation.
 #ifdef SLIME_GEMM_ADD
         if constexpr (true) {
-            const long long off = (long long)(m0 + wm * 128 + r32) * g.ncol + col0 + 4 * half;
+            const long long off = wave_el + f32_lane_elem(lane, g.ncol);
             store_tile_f32_add(acc, static_cast<float*>(g.out[plane]) + off, add + off, g.ncol);
         } else
 #endif
         if constexpr (kBf16) {
-            char* obase = reinterpret_cast<char*>(reinterpret_cast<bf16_t*>(out) +
-                                                  (long long)(m0 + wm * 128) * g.ncol + col0);
+            char* obase = reinterpret_cast<char*>(reinterpret_cast<bf16_t*>(out) + wave_el);
             // The distinct markers keep the compiler from hoisting the accumulator
             // reads common to the three arms above the switch (all 256 at once).
             switch (g.act[plane]) {
@@ -498,8 +461,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_add_kernel(GemmArgs g, 
                     break;
             }
         } else {
-            float* obase = reinterpret_cast<float*>(out) + (long long)(m0 + wm * 128 + r32) * g.ncol +
-                           col0 + 4 * half;
+            float* obase = reinterpret_cast<float*>(out) + wave_el + f32_lane_elem(lane, g.ncol);
             switch (g.act[plane]) {
                 case 1:
                     asm volatile("; epilogue relu");
