@@ -144,6 +144,20 @@ typedef struct {
 int slime_ca_backward(slime_ca* ca, const void* x_in, const void* target, float* grad_x,
                       const slime_ca_grads* grads, double* loss, void* hip_stream);
 
+/* slime_ca_fitness without a handle and without allocating: no counterpart in the
+ * reference. For callers that cannot call hipMalloc (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid allocation). The partial sums go to a
+ * static device buffer of 32 MiB per GPU that the library holds until the process
+ * ends; B*H*chunks*(D*D + 3T) fp64 partials must fit, with the chunk count lowered
+ * from slime_ca_fitness's when needed (which can change the last bits of the Gram
+ * sums), else SLIME_EINVAL. Every call on a GPU shares that buffer: calls that
+ * overlap on one GPU race. The first call on a device looks up the buffer's
+ * address there (make it outside graph capture). config gives B, G, H, D and
+ * dtype of the history (its other fields are validated but unused); outputs as
+ * slime_ca_fitness; no sweep counts. */
+int slime_ca_fitness_static(const slime_ca_config* config, const void* x_hist, int T,
+                            float* erank, float* coherence, float* fitness, void* stream);
+
 /* Jacobi sweeps used by the last slime_ca_fitness call, B*H ints (host copy). */
 int slime_ca_fitness_sweeps(slime_ca* ca, int* h_sweeps);
 

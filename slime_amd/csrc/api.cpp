@@ -556,6 +556,46 @@ int slime_ca_fitness(slime_ca* h, const void* x_hist, int T, float* erank, float
                        fitness, static_cast<hipStream_t>(stream));
 }
 
+int slime_ca_fitness_static(const slime_ca_config* config, const void* x_hist, int T, float* erank,
+                            float* coherence, float* fitness, void* stream) {
+    int rc = validate(config);
+    if (rc) return rc;
+    if (!x_hist || !erank || !coherence || !fitness)
+        return fail(SLIME_EINVAL, "a tensor pointer is NULL");
+    if (T < 2 || T > 65) return fail(SLIME_EINVAL, "T=%d must be in [2, 65]", T);
+    const slime_ca_config& c = *config;
+    if (fitness_chunks(c.G) < 1) return fail(SLIME_EINVAL, "grid too small for the fitness pass");
+    const int chunks = fitness_static_chunks(c.B, c.G, c.D, T);
+    if (chunks < 1)
+        return fail(SLIME_EINVAL,
+                    "B=%d, D=%d, T=%d needs %zu bytes of partial sums, more than the %zu-byte "
+                    "static scratch of slime_ca_fitness_static (use slime_ca_fitness)",
+                    c.B, c.D, T, fitness_partial_bytes(c.B, c.D, T, 1), kFitnessScratchBytes);
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev < 1)
+        return fail(SLIME_ENODEV, "no HIP device visible");
+    void* scr = nullptr;
+    const hipError_t e = fitness_static_scratch(&scr);
+    if (e == hipErrorNoBinaryForGpu) return fail(SLIME_ENODEV, "the current device is not a gfx950");
+    HIP_TRY(e);
+    FitnessArgs f{};
+    f.hist = x_hist;
+    f.t_stride = (long long)c.B * c.G * c.G * c.H * c.D * (c.dtype == SLIME_BF16 ? 2 : 4);
+    f.T = T;
+    f.B = c.B;
+    f.G = c.G;
+    f.D = c.D;
+    f.chunks = chunks;
+    f.gram_part = static_cast<double*>(scr);
+    f.mom_part = f.gram_part + (size_t)c.B * c.H * chunks * c.D * c.D;
+    f.erank = erank;
+    f.coh = coherence;
+    f.fitness = fitness;
+    f.sweeps = nullptr;
+    HIP_TRY(launch_fitness(c.dtype, f, static_cast<hipStream_t>(stream)));
+    return SLIME_OK;
+}
+
 int slime_ca_fitness_sweeps(slime_ca* h, int* h_sweeps) {
     int rc = use_handle(h);
     if (rc) return rc;

@@ -19,9 +19,20 @@
 // Gram and moment partials, then one wave per (batch, head) that reduces them in
 // fixed order, runs the cyclic Jacobi on the fp64 matrix in LDS, and finishes
 // rank, coherence and fitness.
+#include <cstring>
+#include <mutex>
+
 #include "common.hpp"
 #include "fp64.hpp"
 #include "kernels.hpp"
+
+// Scratch of the allocation-free entry point slime_ca_fitness_static: the Gram and
+// moment partials of one call. One copy per GPU, created when the code object loads
+// on that device and held until the process ends; every call on a GPU shares it, so
+// calls that overlap on one GPU race. Host code never takes the array's name as an
+// address (on the host it is only a stand-in for the symbol): fitness_static_scratch
+// looks the device address up once per device and kernels receive that pointer.
+static __device__ __align__(256) unsigned char scratch[slime::kFitnessScratchBytes];
 
 namespace slime {
 namespace {
@@ -427,6 +438,41 @@ int fitness_chunks(int G) {
 
 hipError_t launch_fitness(int dtype, const FitnessArgs& f, hipStream_t s) {
     return dtype == 1 ? launch_t<bf16_t>(f, s) : launch_t<float>(f, s);
+}
+
+size_t fitness_partial_bytes(int B, int D, int T, int chunks) {
+    return (size_t)B * kHeads * chunks * ((size_t)D * D + 3 * (size_t)T) * sizeof(double);
+}
+
+int fitness_static_chunks(int B, int G, int D, int T) {
+    const long long stages = (long long)G * G / kCellsPerStage;
+    for (int c = fitness_chunks(G); c >= 1; --c)
+        if (stages % c == 0 && fitness_partial_bytes(B, D, T, c) <= kFitnessScratchBytes) return c;
+    return 0;
+}
+
+hipError_t fitness_static_scratch(void** ptr) {
+    constexpr int kMaxDevices = 64;
+    static std::mutex mu;
+    static void* addr[kMaxDevices] = {};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[dev]) {
+        hipDeviceProp_t prop;
+        e = hipGetDeviceProperties(&prop, dev);
+        if (e != hipSuccess) return e;
+        if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return hipErrorNoBinaryForGpu;
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        if (!p) return hipErrorInvalidSymbol;
+        addr[dev] = p;
+    }
+    *ptr = addr[dev];
+    return hipSuccess;
 }
 
 }  // namespace slime

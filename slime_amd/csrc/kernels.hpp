@@ -103,6 +103,17 @@ struct FitnessArgs {
 };
 int fitness_chunks(int G);
 hipError_t launch_fitness(int dtype, const FitnessArgs& a, hipStream_t s);
+// Allocation-free fitness (slime_ca_fitness_static): the partial sums live in a
+// static device buffer of kFitnessScratchBytes per GPU. fitness_static_chunks: the
+// largest chunk count <= fitness_chunks(G) that divides the grid's 64-cell stages
+// and whose [B*H][chunks] Gram and moment partials fit in that buffer (0: none
+// fits). fitness_static_scratch: the buffer's device address on the current device
+// (hipErrorNoBinaryForGpu unless it is a gfx950), looked up on the device's first
+// call and cached.
+constexpr size_t kFitnessScratchBytes = size_t(32) << 20;
+size_t fitness_partial_bytes(int B, int D, int T, int chunks);
+int fitness_static_chunks(int B, int G, int D, int T);
+hipError_t fitness_static_scratch(void** ptr);
 
 // ---- backward of one step under the MSE loss (backward.hip) --------------------------------
 struct BackwardArgs {
