@@ -224,8 +224,6 @@ __device__ __forceinline__ void tile_rows(const GemmArgs& g, int tile, int nN, c
     *w = reinterpret_cast<const char*>(static_cast<const T*>(g.Bt) + we);
 }
 
-// Scheduling-group masks (LLVM AMDGPU IGroupLP): MFMA and LDS-read instructions.
-constexpr int kSchedMfma = 0x008, kSchedDsRead = 0x100;
 
 // One slab step: slab kt of the current tile sits in stage S and its fragments in
 // `f` (one register set per 32-byte half kk). The MFMAs of half 0 go first; then
@@ -242,7 +240,6 @@ template <typename T, int S, bool kFirstSlab, bool kReadNext>
 __device__ __forceinline__ void slab_step(const Walk& wk, int kt, int wave, unsigned char* lds,
                                           const FragBase& fb, f32x16 (&acc)[4][4], Frags& f,
                                           int younger) {
-    constexpr int kPer = sizeof(T) == 2 ? 1 : 4;  // MFMA instructions per group
     __builtin_amdgcn_sched_barrier(0);
     static_for<0, 16>([&](auto m) {
         constexpr int M = decltype(m)::value;
@@ -252,23 +249,24 @@ __device__ __forceinline__ void slab_step(const Walk& wk, int kt, int wave, unsi
     lds_barrier();  // slab kt+1 is in LDS; every wave is done reading stage S
     const int ks = kt + 4;
     const bool same = ks < wk.nk;
-    issue_slab(same ? wk.x_cur : wk.x_nxt, same ? wk.w_cur : wk.w_nxt, wk.row_bytes,
-               same ? ks : ks - wk.nk, wave, wk.voff, lds_addr(lds + S * kStageB));
+    // The half-1 MFMAs go out in pairs, each pair after one direct load of slab kt+4
+    // and one fragment read of slab kt+1: when the memory pipeline is backed up and
+    // a load waits to issue, the matrix core still has the previous pair queued.
+    const char* xs = same ? wk.x_cur : wk.x_nxt;
+    const char* ws = same ? wk.w_cur : wk.w_nxt;
+    const long long k_off = dma_k_off(same ? ks : ks - wk.nk);
+    const unsigned sb = lds_addr(lds + S * kStageB);
     const unsigned char* rd = lds + ((S + 1) & 3) * kStageB;
-    if constexpr (kReadNext)
-        static_for<0, 8>([&](auto r) { read_frag<decltype(r)::value>(f, rd, fb); });
-    static_for<16, 32>([&](auto m) {
-        constexpr int M = decltype(m)::value;
-        mfma_group<T, false, M>(acc, f);
+    static_for<0, kDmaPerSlab>([&](auto jj) {
+        constexpr int j = decltype(jj)::value;
+        __builtin_amdgcn_sched_barrier(0);
+        dma16((j < 4 ? xs : ws) + dma_grp_off(j, wave, wk.row_bytes) + k_off, wk.voff, sb + dma_lds_off(j, wave));
+        if constexpr (kReadNext) read_frag<j>(f, rd, fb);
+        mfma_group<T, false, 16 + 2 * j>(acc, f);
+        mfma_group<T, false, 17 + 2 * j>(acc, f);
+        __builtin_amdgcn_sched_barrier(0);
     });
-    if constexpr (kReadNext) {
-        static_for<8, 16>([&](auto r) { read_frag<decltype(r)::value>(f, rd, fb); });
-        static_for<0, 8>([&](auto) {
-            __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2 * kPer, 0);
-        });
-        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 8, 0);
-    }
+    if constexpr (kReadNext) static_for<8, 16>([&](auto r) { read_frag<decltype(r)::value>(f, rd, fb); });
     __builtin_amdgcn_sched_barrier(0);
 }
 
