@@ -56,7 +56,25 @@ def load_traffic(kernel: str, workload: str):
         return None
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (as lscpu reports it, from /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
 def cpu_baseline(cfg, params, X, seconds: float):
+    """The CPU oracle on batch entry 0 of the workload: one warm-up step, then five
+    samples of k steps each (k sized so the five take about `seconds`); the median
+    sample's rate."""
+    import statistics
+
     import numpy as np
 
     import oracle
@@ -65,21 +83,25 @@ def cpu_baseline(cfg, params, X, seconds: float):
                                growth_per_cell=cfg.growth_per_cell, dt=cfg.dt)
     p = {k: (round_bf16(v[:1]) if k in ("WP", "WI", "WV") else v[:1]) for k, v in params.items()}
     x1 = np.ascontiguousarray(X[0:1])
-    oracle.step(ocfg, x1, p, 1)  # warm-up (page-in, thread pool)
-    n, t = 0, 0.0
-    while t < seconds and n < 50:
+    t0 = time.perf_counter()
+    oracle.step(ocfg, x1, p, 1)  # warm-up (page-in, thread pool); sizes the samples
+    k = max(1, int(round(seconds / 5 / (time.perf_counter() - t0))))
+    per_step = []
+    for _ in range(5):
         t0 = time.perf_counter()
-        oracle.step(ocfg, x1, p, 1)
-        t += time.perf_counter() - t0
-        n += 1
+        oracle.step(ocfg, x1, p, k)
+        per_step.append((time.perf_counter() - t0) / k)
+    med = statistics.median(per_step)
     cells = cfg.G * cfg.G
     return {
-        "value": cells * n / t,
+        "value": cells / med,
         "unit": "cell-updates/s",
         "cores": oracle.num_threads(),
         "kind": "port",
-        "sample": f"CPU oracle (fp64, OpenMP) on batch entry 0 of the same workload: "
-                  f"{n} step(s) of {cells} cells in {t:.1f} s",
+        "cpu_model": cpu_model(),
+        "sample": f"CPU oracle (fp64, OpenMP) on batch entry 0 of the same workload "
+                  f"({cells} cells): 1 warm-up step, then the median of 5 samples of {k} "
+                  f"step(s) each ({min(per_step) * 1e3:.0f}-{max(per_step) * 1e3:.0f} ms per step)",
     }
 
 
@@ -246,8 +268,9 @@ def bench_backward(args) -> int:
 
 
 def bench_ensemble(args) -> int:
-    """c4: 16 pods with independent weights, batch entry = pod,
-    8 steps, then the fused fitness over the 8-state history; prints one JSON line."""
+    """c4: 16 pods with independent weights, batch entry = pod, an 8-state history
+    by slime_ca_rollout (the single-step calls timed beside it), then the fused
+    fitness over it; prints one JSON line."""
     import torch
 
     from slime_amd import CONFIGS, Pseudopod, make_params, make_state
@@ -260,18 +283,25 @@ def bench_ensemble(args) -> int:
     with Pseudopod(cfg.B, cfg.G, cfg.H, cfg.D, cfg.dtype, cfg.dt, False, cfg.pods) as ca:
         ca.set_params(p)
         hist = torch.empty((T,) + tuple(x0.shape), dtype=torch.bfloat16, device="cuda")
+        box = {}
 
-        def rollout():
+        def rollout():  # slime_ca_rollout: each state kept before its mass rescale
+            hist[0].copy_(x0)
+            box["scales"] = ca.rollout(hist)
+
+        def single_steps():  # T - 1 calls of slime_ca_step, each rescaling its output
             hist[0].copy_(x0)
             for i in range(1, T):
                 ca.forward(hist[i - 1], out=hist[i])
 
+        single_steps()
         rollout()
-        ca.fitness(hist)
+        ca.fitness_scaled(hist, box["scales"])
         reps = max(args.steps // 2, 1)
+        single_ms = _time(single_steps, reps)
         roll_ms = _time(rollout, reps)
-        fit_ms = _time(lambda: ca.fitness(hist), reps * 4)
-        er, coh, fit = ca.fitness(hist)
+        fit_ms = _time(lambda: ca.fitness_scaled(hist, box["scales"]), reps * 4)
+        er, coh, fit = ca.fitness_scaled(hist, box["scales"])
         torch.cuda.synchronize()
     steps = T - 1
     out = {"metric": "c4 ensemble: step throughput and fused fitness latency",
@@ -280,7 +310,8 @@ def bench_ensemble(args) -> int:
            "config": {"workload": "c4", "pods": cfg.pods, "grid": cfg.G, "batch": cfg.B,
                       "history": T},
            "value": cfg.cell_updates_per_step * steps / (roll_ms * 1e-3),
-           "rollout_ms": roll_ms, "steps": steps, "fitness_us": fit_ms * 1e3,
+           "rollout_ms": roll_ms, "single_step_calls_ms": single_ms, "steps": steps,
+           "fitness_us": fit_ms * 1e3,
            "fitness_mean": float(fit.mean()), "erank_mean": float(er.mean()),
            "coherence_mean": float(coh.mean())}
     print(json.dumps(out), flush=True)

@@ -144,6 +144,26 @@ typedef struct {
 int slime_ca_backward(slime_ca* ca, const void* x_in, const void* target, float* grad_x,
                       const slime_ca_grads* grads, double* loss, void* hip_stream);
 
+/* T-1 steps from hist[0] with every state kept: the organism's run of generations
+ * whose last states the fitness scores (slime/core/organism.cu:679-683, the
+ * effective-rank history; slime/kernels/warp_ca.cu:178-185 scores such a history).
+ * hist (device, [T][B][G][G][C], the handle's dtype) holds the initial state in
+ * hist[0] on entry; on return hist[t] holds state t as the step that produced it
+ * stores it before its mass rescale, and scales (device fp64, [T][B][H]) the factor
+ * that completes it: state t = scales[t][b][h] * hist[t] over head h of batch entry
+ * b (scales[0] = 1). The next step reads each state that way, so no state is
+ * rescaled in a pass of its own. Up to the storage rounding (once per state, before
+ * rather than after the factor), the states are those of T-1 calls of
+ * slime_ca_step(n_steps = 1); slime_ca_fitness_scaled scores the history. The
+ * handle's mass sums are those of the last step. */
+int slime_ca_rollout(slime_ca* ca, void* hist, int T, double* scales, void* stream);
+
+/* slime_ca_fitness of a history stored with per-(state, batch, head) factors as
+ * slime_ca_rollout leaves it: the moments and the last state's Gram are scaled in
+ * fp64, so the result is that of the states scales[t] * hist[t]. */
+int slime_ca_fitness_scaled(slime_ca* ca, const void* x_hist, const double* scales, int T,
+                            float* erank, float* coherence, float* fitness, void* stream);
+
 /* slime_ca_fitness without a handle and without allocating: no counterpart in the
  * reference. For callers that cannot call hipMalloc (code under HIP graph capture,
  * tight serving loops, harnesses that forbid allocation). The partial sums go to a

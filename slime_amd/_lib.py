@@ -27,7 +27,8 @@ EXPORTS = (
     "slime_ca_uses_mfma", "slime_ca_set_timing", "slime_ca_timings", "slime_ca_last_error",
     "slime_neural_ca_update", "slime_ca_backward", "slime_pool_init", "slime_pool_set_fitness",
     "slime_ca_hunger", "slime_pool_age", "slime_pool_cull", "slime_pool_spawn", "slime_pool_spawn_wave",
-    "slime_pool_evolve", "slime_snapshot_json", "slime_ca_fitness_static",
+    "slime_pool_evolve", "slime_snapshot_json", "slime_ca_fitness_static", "slime_ca_rollout",
+    "slime_ca_fitness_scaled",
 )
 
 

@@ -193,6 +193,37 @@ class Pseudopod:
                                              *[_ptr(o) for o in outs], _stream(stream)))
         return tuple(outs)
 
+    def rollout(self, hist, stream=None):
+        """T-1 steps from ``hist[0]`` into ``hist`` ([T, B, G, G, C], in place), each state
+        stored before its mass rescale (slime_ca_rollout). Returns the factors, a float64
+        CUDA tensor [T, B, H]: state t = factor[t, b, h] * hist[t] over head h."""
+        torch = _torch()
+        if hist.dim() != 5 or tuple(hist.shape[1:]) != self.state_shape \
+                or hist.dtype != self.torch_dtype or not hist.is_contiguous():
+            raise ValueError(f"hist must be [T, {', '.join(map(str, self.state_shape))}] "
+                             f"{self.torch_dtype}")
+        scales = torch.empty((hist.shape[0], self.B, self.H), dtype=torch.float64, device="cuda")
+        _lib.check(self.lib.slime_ca_rollout(self._h, _ptr(hist), int(hist.shape[0]), _ptr(scales),
+                                             _stream(stream)))
+        return scales
+
+    def fitness_scaled(self, hist, scales, stream=None):
+        """fitness of a history left by ``rollout``: (erank, coherence, fitness), [B, H] each."""
+        torch = _torch()
+        if hist.dim() != 5 or tuple(hist.shape[1:]) != self.state_shape \
+                or hist.dtype != self.torch_dtype or not hist.is_contiguous():
+            raise ValueError(f"hist must be [T, {', '.join(map(str, self.state_shape))}] "
+                             f"{self.torch_dtype}")
+        if tuple(scales.shape) != (hist.shape[0], self.B, self.H) or scales.dtype != torch.float64 \
+                or not scales.is_contiguous():
+            raise ValueError("scales must be a contiguous float64 tensor [T, B, H]")
+        outs = [torch.empty((self.B, self.H), dtype=torch.float32, device="cuda")
+                for _ in range(3)]
+        _lib.check(self.lib.slime_ca_fitness_scaled(self._h, _ptr(hist), _ptr(scales),
+                                                    int(hist.shape[0]), *[_ptr(o) for o in outs],
+                                                    _stream(stream)))
+        return tuple(outs)
+
     def effective_rank(self, hist, stream=None):
         return self.fitness(hist, stream)[0]
 

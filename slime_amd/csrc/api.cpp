@@ -254,7 +254,8 @@ int run_project(slime_ca* h, const void* x, const float* x_scale, void* P, void*
 // S2-S6 plus the mass partials and S7 finalize: y_raw gets the unscaled output,
 // out_scale the per-(b, head) conservation factor.
 int run_stencil(slime_ca* h, const void* x, const float* x_scale, const void* P, const void* I,
-                const void* V, void* y_raw, int y_f32, float* out_scale, hipStream_t s) {
+                const void* V, void* y_raw, int y_f32, float* out_scale, hipStream_t s,
+                double* out_scale64 = nullptr) {
     const slime_ca_config& c = h->cfg;
     StencilArgs a{};
     a.X = x;
@@ -279,14 +280,14 @@ int run_stencil(slime_ca* h, const void* x, const float* x_scale, const void* P,
     a.dt = c.dt;
     HIP_TRY(timed(h, h->stencil_ev, s, [&] { return launch_stencil(c.dtype, a, s); }));
     HIP_TRY(launch_mass_finalize(h->part_in, h->part_out, c.B * c.H, h->tiles, h->mass_in,
-                                 h->mass_out, out_scale, s));
+                                 h->mass_out, out_scale, out_scale64, s));
     return SLIME_OK;
 }
 
 
 // E1-E5 over T states, state t at x_hist + t * t_stride bytes.
 int run_fitness(slime_ca* h, const void* x_hist, long long t_stride, int T, float* erank,
-                float* coherence, float* fitness, hipStream_t s) {
+                float* coherence, float* fitness, hipStream_t s, const double* scales = nullptr) {
     const slime_ca_config& c = h->cfg;
     const size_t BH = (size_t)c.B * c.H;
     const int chunks = fitness_chunks(c.G);
@@ -321,6 +322,7 @@ int run_fitness(slime_ca* h, const void* x_hist, long long t_stride, int T, floa
     f.coh = coherence;
     f.fitness = fitness;
     f.sweeps = h->sweeps;
+    f.scales = scales;
     HIP_TRY(launch_fitness(c.dtype, f, s));
     return SLIME_OK;
 }
@@ -554,6 +556,47 @@ int slime_ca_fitness(slime_ca* h, const void* x_hist, int T, float* erank, float
     if (T < 2 || T > 65) return fail(SLIME_EINVAL, "T=%d must be in [2, 65]", T);
     return run_fitness(h, x_hist, h->state_elems * (long long)h->elem, T, erank, coherence,
                        fitness, static_cast<hipStream_t>(stream));
+}
+
+int slime_ca_rollout(slime_ca* h, void* hist, int T, double* scales, void* stream) {
+    int rc = use_handle(h);
+    if (rc) return rc;
+    if (!h->params_set) return fail(SLIME_ESTATE, "slime_ca_set_params has not been called");
+    if (!hist || !scales) return fail(SLIME_EINVAL, "a tensor pointer is NULL");
+    if (T < 2 || T > 65) return fail(SLIME_EINVAL, "T=%d must be in [2, 65]", T);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    h->last_stream = s;
+    const slime_ca_config& c = h->cfg;
+    const int BH = c.B * c.H;
+    const size_t state_bytes = (size_t)h->state_elems * h->elem;
+    char* base = static_cast<char*>(hist);
+    HIP_TRY(launch_fill_f64(scales, BH, 1.0, s));
+    // Step t reads state t-1 as stored, with its factor folded into the weights and
+    // the stencil's loads, and stores state t before its own rescale; the factor goes
+    // to the handle (for step t+1) and to scales[t].
+    const float* cur_scale = h->unit_scale;
+    for (int t = 1; t < T; ++t) {
+        const void* cur = base + (size_t)(t - 1) * state_bytes;
+        void* y = base + (size_t)t * state_bytes;
+        float* ys = h->scale[t & 1];
+        rc = run_project(h, cur, cur_scale, h->P, h->I, h->V, s);
+        if (rc) return rc;
+        rc = run_stencil(h, cur, cur_scale, h->P, h->I, h->V, y, 0, ys, s, scales + (size_t)t * BH);
+        if (rc) return rc;
+        cur_scale = ys;
+    }
+    return SLIME_OK;
+}
+
+int slime_ca_fitness_scaled(slime_ca* h, const void* x_hist, const double* scales, int T,
+                            float* erank, float* coherence, float* fitness, void* stream) {
+    int rc = use_handle(h);
+    if (rc) return rc;
+    if (!x_hist || !scales || !erank || !coherence || !fitness)
+        return fail(SLIME_EINVAL, "a tensor pointer is NULL");
+    if (T < 2 || T > 65) return fail(SLIME_EINVAL, "T=%d must be in [2, 65]", T);
+    return run_fitness(h, x_hist, h->state_elems * (long long)h->elem, T, erank, coherence,
+                       fitness, static_cast<hipStream_t>(stream), scales);
 }
 
 int slime_ca_fitness_static(const slime_ca_config* config, const void* x_hist, int T, float* erank,

@@ -271,6 +271,11 @@ __global__ __launch_bounds__(64) void fitness_finalize_kernel(FitnessArgs f) {
     const bool own = D == kWave || lane < D;  // lane owns row/column `lane` of the matrix
     const double ncell = (double)f.G * f.G;
     const double tol = 1e-6;
+    const int BH = gridDim.x;
+    // Per-state factors of a rolled-out history (1 when the states are stored as they are).
+    auto scale_of = [&](int t) { return f.scales ? f.scales[(long long)t * BH + bh] : 1.0; };
+    const double s_last = scale_of(f.T - 1);
+    const double gram_scale = s_last * s_last / ncell;
 
     // Fixed-order reduction of the Gram partials: element e sums chunks 0, 1, ... in
     // turn; kE elements per lane at once keep the loads independent.
@@ -289,7 +294,7 @@ __global__ __launch_bounds__(64) void fitness_finalize_kernel(FitnessArgs f) {
 #pragma unroll
             for (int k = 0; k < kE; ++k) {
                 const int e = e0 + k * 64 + lane;
-                A[(e / D) * kLd + e % D] = s[k] / ncell;
+                A[(e / D) * kLd + e % D] = f.scales ? s[k] * gram_scale : s[k] / ncell;
             }
         }
     }
@@ -368,6 +373,14 @@ __global__ __launch_bounds__(64) void fitness_finalize_kernel(FitnessArgs f) {
             m[2] += q[t * 3 + 2];
             m[3] += q[(t - 1) * 3 + 1];
             m[4] += q[t * 3 + 1];
+        }
+        if (f.scales) {
+            const double sa = scale_of(t - 1), sb = scale_of(t);
+            m[0] *= sa;
+            m[1] *= sb;
+            m[2] *= sa * sb;
+            m[3] *= sa * sa;
+            m[4] *= sb * sb;
         }
         const double cov = m[2] - m[0] * m[1] / n;
         const double va = m[3] - m[0] * m[0] / n;

@@ -80,9 +80,11 @@ hipError_t launch_stencil(int dtype, const StencilArgs& a, hipStream_t s);
 // fp64 ratio, scale_out[1][b][h] the fp32 rounding of the rest. A scale applied
 // as x * hi + x * lo carries no rounding bias from step to step, so the mass of a
 // long chain of steps does not drift with the rounding of the ratio.
+// scale64_out (may be nullptr): the same factor as one fp64 value per (b, h).
 hipError_t launch_mass_finalize(const double* part_in, const double* part_out, int BH, int tiles,
                                 double* mass_in, double* mass_out, float* scale_out,
-                                hipStream_t s);
+                                double* scale64_out, hipStream_t s);
+hipError_t launch_fill_f64(double* p, int n, double v, hipStream_t s);
 // y[i] = cvt((scale[0][b][h] + scale[1][b][h]) * x[i]) over the whole state; x is
 // fp32 when x_f32 is set, else in the storage type.
 hipError_t launch_rescale(int dtype, const void* x, int x_f32, const float* scale, void* y, int B,
@@ -100,6 +102,9 @@ struct FitnessArgs {
     float* coh;
     float* fitness;
     int* sweeps;        // [B][H] Jacobi sweeps used (may be nullptr)
+    // [T][B*H] (may be nullptr): state t of the history is scales[t] times the stored
+    // values per (b, h); the moments and the last state's Gram are scaled in fp64.
+    const double* scales;
 };
 int fitness_chunks(int G);
 hipError_t launch_fitness(int dtype, const FitnessArgs& a, hipStream_t s);

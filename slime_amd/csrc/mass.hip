@@ -44,7 +44,7 @@ namespace {
 __global__ __launch_bounds__(64) void mass_finalize_kernel(const double* part_in,
                                                            const double* part_out, int tiles,
                                                            double* mass_in, double* mass_out,
-                                                           float* scale_out) {
+                                                           float* scale_out, double* scale64_out) {
     // One wave per (b, h): lanes stride over tiles, then a fixed-shape tree.
     __shared__ double s_in[64], s_out[64];
     const int bh = blockIdx.x, lane = threadIdx.x;
@@ -69,6 +69,7 @@ __global__ __launch_bounds__(64) void mass_finalize_kernel(const double* part_in
         const float hi = (float)r, lo = (float)(r - (double)hi);
         scale_out[bh] = hi;
         scale_out[gridDim.x + bh] = lo;
+        if (scale64_out) scale64_out[bh] = (double)hi + (double)lo;
         mass_in[bh] = in;
         mass_out[bh] = ((double)hi + (double)lo) * out;
     }
@@ -108,9 +109,21 @@ __global__ __launch_bounds__(256) void rescale_kernel(const TI* x, const float* 
 
 hipError_t launch_mass_finalize(const double* part_in, const double* part_out, int BH, int tiles,
                                 double* mass_in, double* mass_out, float* scale_out,
-                                hipStream_t s) {
+                                double* scale64_out, hipStream_t s) {
     hipLaunchKernelGGL(mass_finalize_kernel, dim3(BH), dim3(64), 0, s, part_in, part_out, tiles,
-                       mass_in, mass_out, scale_out);
+                       mass_in, mass_out, scale_out, scale64_out);
+    return hipGetLastError();
+}
+
+namespace {
+__global__ __launch_bounds__(256) void fill_f64_kernel(double* p, int n, double v) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+}  // namespace
+
+hipError_t launch_fill_f64(double* p, int n, double v, hipStream_t s) {
+    hipLaunchKernelGGL(fill_f64_kernel, dim3((n + 255) / 256), dim3(256), 0, s, p, n, v);
     return hipGetLastError();
 }
 

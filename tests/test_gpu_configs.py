@@ -247,3 +247,64 @@ def test_fitness_multi_stage_chunks(oracle, dtype, G):
     np.testing.assert_allclose(er, rer, rtol=1e-6, atol=1e-6)
     np.testing.assert_allclose(coh, rcoh, atol=1e-6)
     np.testing.assert_allclose(fit, rfit, rtol=1e-6, atol=1e-6)
+
+
+def test_c4_rollout_matches_oracle_and_single_steps(oracle):
+    """slime_ca_rollout on the c4 workload: 7 steps into an 8-state history, each state
+    stored before its mass rescale with its factor in `scales`. The completed states
+    (factor x stored values) are checked step by step against the oracle from the
+    previous completed state (2e-2), their head sums against the input's (1e-6: the
+    factor is applied in fp64 here, so the bf16 storage rounding does not enter the
+    sums), the first state against the single-step path (the two differ only in where
+    the bf16 rounding falls: before or after the factor, at most one bf16 unit), and
+    the scaled fitness against the oracle's fitness of the completed states (1e-6,
+    equal Jacobi sweep counts)."""
+    cfg = CONFIGS["c4"]
+    p = make_params(cfg, seed=1)
+    p = {k: (round_bf16(v) if k in ("WP", "WI", "WV") else v) for k, v in p.items()}
+    X1 = round_bf16(make_state(cfg, seed=2, B=1))
+    T = cfg.steps
+    with _engine(cfg) as e:
+        e.set_params(p)
+        x0 = torch.from_numpy(X1).cuda().to(torch.bfloat16).expand(cfg.B, -1, -1, -1).contiguous()
+        hist = torch.empty((T,) + tuple(x0.shape), dtype=torch.bfloat16, device="cuda")
+        hist[0] = x0
+        scales = e.rollout(hist)
+        er, coh, fit = e.fitness_scaled(hist, scales)
+        torch.cuda.synchronize()
+        sweeps = e.jacobi_sweeps()
+        y1 = e.forward(x0)  # the single-step path's first state
+        torch.cuda.synchronize()
+        S = scales.cpu().numpy()
+        true = hist.double().view(T, cfg.B, cfg.G * cfg.G, cfg.H, cfg.D) * scales.view(T, cfg.B, 1, cfg.H, 1)
+        sums = true.sum(dim=(2, 4)).cpu().numpy()
+        truef = true.float().view(T, cfg.B, cfg.G, cfg.G, cfg.C).cpu().numpy()
+        del true
+        Y1 = y1.float().cpu().numpy()
+        er, coh, fit = (v.cpu().numpy() for v in (er, coh, fit))
+    assert np.all(S[0] == 1.0) and np.all(S > 0)
+    drift = np.max(np.abs(sums[1:] - sums[0]) / np.abs(sums[0]))
+    print(f"  rollout: factors in [{S[1:].min():.6f}, {S[1:].max():.6f}], head-mass drift over 7 steps {drift:.2e}")
+    assert drift <= 1e-6
+    e1 = norm_err(truef[1], Y1)
+    print(f"  first state against the single-step path: normalised difference {e1:.2e}")
+    assert e1 <= 2.0 ** -7
+    one = _ocfg(cfg, B=1, pods=1)
+    worst = 0.0
+    for t in range(1, T):
+        for pod in sorted({(3 * t) % cfg.pods, (5 * t + 2) % cfg.pods}):
+            ref, _, _ = oracle.step(one, truef[t - 1][pod:pod + 1], _pod_params(p, pod), 1)
+            err = norm_err(truef[t][pod:pod + 1], ref)
+            worst = max(worst, err)
+            assert err <= TOL["bf16"], (t, pod, err)
+    print(f"  worst single-step error over the checked pods {worst:.2e}")
+    ocfg = _ocfg(cfg)
+    rer, rcoh, rfit = oracle.fitness(ocfg, truef)
+    gram = oracle.gram(ocfg, truef[-1])
+    rsweeps = np.array([[oracle.jacobi_eigs(gram[b, h])[1] for h in range(cfg.H)]
+                        for b in range(cfg.B)])
+    print(f"  fitness: max |d erank| {np.max(np.abs(er - rer)):.2e}, max |d coh| {np.max(np.abs(coh - rcoh)):.2e}")
+    np.testing.assert_array_equal(sweeps, rsweeps)
+    np.testing.assert_allclose(er, rer, rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(coh, rcoh, atol=1e-6)
+    np.testing.assert_allclose(fit, rfit, rtol=1e-6, atol=1e-6)
