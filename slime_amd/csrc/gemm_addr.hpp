@@ -21,14 +21,20 @@ constexpr int kSlabB = 64;                     // bytes of K per tile row per sl
 constexpr int kStages = 4;                     // LDS ring depth (slabs)
 constexpr int kStageB = (kBM + kBN) * kSlabB;  // 32 KiB
 constexpr int kDmaPerSlab = 8;                 // direct-load instructions per wave per slab
-constexpr int kEpiRowB = 144;                  // bf16 epilogue staging row pitch
+constexpr int kEpiRowB = 128;                  // bf16 epilogue staging row pitch (no padding)
 constexpr int kEpiWaveB = 32 * kEpiRowB;       // staging bytes per wave
 constexpr int kStoresBf16 = 32;                // global stores per wave per tile (bf16 epilogue)
 constexpr int kStoresF32 = 64;                 // global stores per wave per tile (fp32 epilogue)
 
 // Stage layout: tile row r (0..255 cells, 256..511 output channels) holds its 64
-// slab bytes at r*64 as four 16-byte chunks, physical chunk = logical chunk ^ f(r).
-SLIME_HD constexpr int row_swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+// slab bytes at r*64 as four 16-byte chunks, physical chunk = logical chunk ^ f(r),
+// f(r) = (r >> 2) & 3. gfx950 serves a 16-byte LDS read of a wave in four passes of
+// 16 lanes -- the lanes 4q..4q+3 of the quads q that share q >> 3 and the parity of
+// q & 7 -- over 16 bank groups of 16 bytes (address / 16 % 16), measured with the
+// bank-conflict counter. With this f the 16 lanes of every pass of a fragment read
+// (row lane % 32 of a block, logical chunk 2 kk + lane / 32) fall in 16 distinct
+// groups: no conflict cycles.
+SLIME_HD constexpr int row_swz(int r) { return (r >> 2) & 3; }
 
 // One persistent workgroup per CU, never more than there are tiles.
 SLIME_HD int grid_size(int ntiles, int n_cu) { return ntiles < n_cu ? ntiles : n_cu; }
@@ -105,15 +111,25 @@ SLIME_HD unsigned frag_w_off(int kk, int lane, int wave) {
 }
 SLIME_HD unsigned frag_block_off(int q) { return (unsigned)(q * 32 * kSlabB); }
 
-// bf16 epilogue staging in the per-wave region: lane writes 8 bytes at
-// epi_w_off + (ii * 32 + 8 q) * 2 (ii < 2, q < 4) and reads 16 bytes at
-// epi_r_off + s4 * 8 * kEpiRowB (s4 < 4).
+// bf16 epilogue staging in the per-wave region (32 rows of 64 channels, 128 bytes).
+// Row r keeps its eight 16-byte chunks (8 channels each) at physical chunk = logical
+// chunk ^ (r & 7), and the two 8-byte halves of a chunk (4 channels each) swapped when
+// bit 3 of r is set. Write: lane (row r = lane % 32, half h = lane / 32) stores its
+// 8 bytes of logical chunk k at epi_w_off(wave, lane) ^ (k << 4) (the XOR only touches
+// the chunk bits). Read: lane l takes row l / 8 + 8 s4, logical chunk l % 8, at
+// epi_r_off(wave, lane) + s4 * 8 * kEpiRowB, halves swapped for odd s4. Every pass of
+// the 8-byte writes (16 lanes over 16 groups of 8 bytes) and of the 16-byte reads
+// falls in distinct bank groups.
 SLIME_HD unsigned epi_w_off(int wave, int lane) {
-    return (unsigned)(wave * kEpiWaveB + (lane & 31) * kEpiRowB + (lane >> 5) * 8);
+    const int r = lane & 31, h = lane >> 5;
+    return (unsigned)(wave * kEpiWaveB + r * kEpiRowB + ((r & 7) << 4) + ((h ^ ((r >> 3) & 1)) << 3));
 }
+SLIME_HD unsigned epi_w_piece(unsigned w_off, int k) { return w_off ^ (unsigned)(k << 4); }
 SLIME_HD unsigned epi_r_off(int wave, int lane) {
-    return (unsigned)(wave * kEpiWaveB + (lane >> 3) * kEpiRowB + (lane & 7) * 16);
+    const int r = lane >> 3;  // row inside each run of 8 rows
+    return (unsigned)(wave * kEpiWaveB + r * kEpiRowB + (((lane & 7) ^ r) << 4));
 }
+SLIME_HD bool epi_r_swapped(int s4) { return (s4 & 1) != 0; }
 
 // Output of a tile: plane n0 / ncol; the wave's first output element in that plane
 // (row m0 + 128 wm, column n0 - plane ncol + 128 wn).

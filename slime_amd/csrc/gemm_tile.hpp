@@ -83,9 +83,6 @@ __device__ __forceinline__ void store_tile_f32_add(f32x16 (&acc)[4][4], float* o
 }
 #endif
 
-// Rows of the per-wave staging region are padded to 144 bytes (kEpiRowB): the
-// 8-byte writes of 16 consecutive rows hit distinct banks.
-
 typedef __attribute__((address_space(3))) void lds_void_t;
 
 // One direct global->LDS load (global_load_lds_dwordx4, SGPR base + 32-bit lane
@@ -315,18 +312,20 @@ __device__ __forceinline__ void convert_tile(f32x16 (&acc)[4][4], OutBuf& ob) {
 }
 
 // Staging of one group: lane (row r32 = lane % 32, half = lane / 32) writes its 8
-// pieces of 4 channels; read back, lane l takes 16 bytes of row l/8 (+8 s4).
+// pieces of 4 channels; read back, lane l takes 16 bytes of row l/8 (+8 s4). The
+// staging layout (gemm_addr.hpp) is free of bank conflicts; rows with bit 3 set hold
+// their chunk halves swapped, undone here in registers.
 template <int Gr>
-__device__ __forceinline__ void stage_write(const OutBuf& ob, unsigned char* wp) {
+__device__ __forceinline__ void stage_write(const OutBuf& ob, unsigned char* epi, unsigned w_off) {
 #pragma unroll
-    for (int ii = 0; ii < 2; ++ii)
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-            *reinterpret_cast<uint2*>(wp + (ii * 32 + 8 * q) * 2) = ob.v[Gr][4 * ii + q];
+    for (int k = 0; k < 8; ++k) *reinterpret_cast<uint2*>(epi + epi_w_piece(w_off, k)) = ob.v[Gr][k];
 }
 __device__ __forceinline__ void stage_read(const unsigned char* rp, uint4 (&tmp)[4]) {
 #pragma unroll
-    for (int s4 = 0; s4 < 4; ++s4) tmp[s4] = *reinterpret_cast<const uint4*>(rp + s4 * 8 * kEpiRowB);
+    for (int s4 = 0; s4 < 4; ++s4) {
+        const uint4 v = *reinterpret_cast<const uint4*>(rp + s4 * 8 * kEpiRowB);
+        tmp[s4] = epi_r_swapped(s4) ? make_uint4(v.z, v.w, v.x, v.y) : v;
+    }
 }
 template <int Gr>
 __device__ __forceinline__ void store_group(char* ob, unsigned gl, int ncol, const uint4 (&tmp)[4]) {
@@ -340,16 +339,16 @@ __device__ __forceinline__ void store_group(char* ob, unsigned gl, int ncol, con
 
 template <int kAct>
 __device__ __forceinline__ void store_tile_bf16(f32x16 (&acc)[4][4], char* ob, int ncol,
-                                                unsigned char* ep_w, const unsigned char* ep_r,
+                                                unsigned char* epi, unsigned ep_w, const unsigned char* ep_r,
                                                 unsigned gl) {
     OutBuf obuf;
     convert_tile<kAct>(acc, obuf);
     uint4 t[2][4];
-    stage_write<0>(obuf, ep_w);
+    stage_write<0>(obuf, epi, ep_w);
     stage_read(ep_r, t[0]);
     static_for<1, 8>([&](auto gc) {
         constexpr int Gr = decltype(gc)::value;
-        stage_write<Gr>(obuf, ep_w);  // LDS keeps each wave's order: after read Gr-1
+        stage_write<Gr>(obuf, epi, ep_w);  // LDS keeps each wave's order: after read Gr-1
         stage_read(ep_r, t[Gr & 1]);
         store_group<Gr - 1>(ob, gl, ncol, t[(Gr - 1) & 1]);
     });
@@ -366,7 +365,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_add_kernel(GemmArgs g, 
     constexpr bool kBf16 = sizeof(T) == 2;
     // bf16 epilogue staging, one region per wave (the stages hold the next tile's
     // first slabs while the epilogue runs).
-    __shared__ __attribute__((aligned(16))) unsigned char epi[kBf16 ? 4 * kEpiWaveB : 16];
+    __shared__ __attribute__((aligned(128))) unsigned char epi[kBf16 ? 4 * kEpiWaveB : 16];
 #ifndef SLIME_GEMM_ADD
     constexpr int kStores = kBf16 ? kStoresBf16 : kStoresF32;
 #else
@@ -409,7 +408,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_add_kernel(GemmArgs g, 
 
     bool stores_pending = false;  // the previous tile's stores follow slabs 0..3 of this one
     f32x16 acc[4][4];
-    unsigned char* ep_w = epi + epi_w_off(wave, lane);
+    const unsigned ep_w = epi_w_off(wave, lane);
     const unsigned char* ep_r = epi + epi_r_off(wave, lane);
     const unsigned ep_gl = epi_gl_off(lane, g.ncol);
     while (true) {
@@ -447,15 +446,15 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_add_kernel(GemmArgs g, 
             switch (g.act[plane]) {
                 case 1:
                     asm volatile("; epilogue relu");
-                    store_tile_bf16<1>(acc, obase, g.ncol, ep_w, ep_r, ep_gl);
+                    store_tile_bf16<1>(acc, obase, g.ncol, epi, ep_w, ep_r, ep_gl);
                     break;
                 case 2:
                     asm volatile("; epilogue gelu");
-                    store_tile_bf16<2>(acc, obase, g.ncol, ep_w, ep_r, ep_gl);
+                    store_tile_bf16<2>(acc, obase, g.ncol, epi, ep_w, ep_r, ep_gl);
                     break;
                 default:
                     asm volatile("; epilogue identity");
-                    store_tile_bf16<0>(acc, obase, g.ncol, ep_w, ep_r, ep_gl);
+                    store_tile_bf16<0>(acc, obase, g.ncol, epi, ep_w, ep_r, ep_gl);
                     break;
             }
         } else {

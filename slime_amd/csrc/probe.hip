@@ -7,9 +7,14 @@
 //   * HBM: 16-byte-per-lane streaming read, write and copy kernels over 2 GiB.
 // It also checks on the device that the short fp64 division and square root of the
 // Jacobi rotation (fp64.hpp) return the bits of IEEE `/` and `sqrt`.
+// LDS bank probes (run under `rocprofv3 --pmc SQ_INSTS_LDS SQ_LDS_BANK_CONFLICT`, one
+// dispatch per call): the projection GEMM's LDS access patterns, the kernel's own
+// address functions (gemm_addr.hpp) beside the layouts it used before, and single-lane
+// displacements of a conflict-free linear pattern, which give the bank model.
 #include <hip/hip_runtime.h>
 
 #include "fp64.hpp"
+#include "gemm_addr.hpp"
 
 #include <stdint.h>
 
@@ -126,9 +131,128 @@ __global__ void fp64_core_check(long long n, uint64_t seed, unsigned long long* 
     if (miss) atomicAdd(bad, miss);
 }
 
+typedef __attribute__((ext_vector_type(2))) unsigned int u32x2;
+
+// One workgroup of 4 waves per CU, 256 workgroups, each running `iters` rounds of one
+// access pattern over 64 KiB of LDS. kind: 0 linear 16-byte reads; 1 the GEMM's
+// fragment reads (16 per round); 2 the same reads under the GEMM's earlier row
+// swizzle ((r >> 1) ^ (r >> 3)) & 3; 3 the GEMM's epilogue staging writes (8 per
+// round); 4 its staging reads (4 per round); 5 and 6 the earlier staging layout
+// (144-byte rows, no swizzle) writes and reads. Every 8-byte write has its own
+// address register, so no two are merged into one instruction.
+template <int kKind>
+__global__ __launch_bounds__(256) void lds_pattern(unsigned* sink, int iters) {
+    using namespace slime::gemm_addr;
+    __shared__ __attribute__((aligned(1024))) unsigned char lds[65536];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int i = tid; i < 65536 / 16; i += 256) reinterpret_cast<u32x4*>(lds)[i] = u32x4{(unsigned)i, 1u, 2u, 3u};
+    __syncthreads();
+    const int r32 = lane & 31, half = lane >> 5;
+    u32x4 acc = {0u, 0u, 0u, 0u};
+    for (int it = 0; it < iters; ++it) {
+        asm volatile("" ::"v"(lds) : "memory");  // the stores are observable
+        if constexpr (kKind == 0) {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) acc += *reinterpret_cast<const u32x4*>(lds + wave * 1024 + lane * 16 + j * 4096);
+        } else if constexpr (kKind == 1 || kKind == 2) {
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    unsigned x = frag_x_off(kk, lane, wave) + frag_block_off(q);
+                    unsigned w = frag_w_off(kk, lane, wave) + frag_block_off(q) - kStageB / 2;  // inside 64 KiB
+                    if constexpr (kKind == 2) {  // same rows, the earlier chunk permutation
+                        const unsigned undo = (unsigned)(row_swz(r32) << 4);
+                        const unsigned old = (unsigned)((((r32 >> 1) ^ (r32 >> 3)) & 3) << 4);
+                        x = x ^ undo ^ old;
+                        w = w ^ undo ^ old;
+                    }
+                    acc += *reinterpret_cast<const u32x4*>(lds + x);
+                    acc += *reinterpret_cast<const u32x4*>(lds + w);
+                }
+        } else if constexpr (kKind == 3 || kKind == 5) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                unsigned a = kKind == 3 ? epi_w_piece(epi_w_off(wave, lane), k)
+                                        : (unsigned)(wave * 32 * 144 + r32 * 144 + half * 8 + k * 16);
+                asm volatile("" : "+v"(a));
+                *reinterpret_cast<u32x2*>(lds + a) = u32x2{acc.x + (unsigned)it, (unsigned)k};
+            }
+        } else {
+#pragma unroll
+            for (int s4 = 0; s4 < 4; ++s4) {
+                const unsigned a = kKind == 4 ? epi_r_off(wave, lane) + s4 * 8 * kEpiRowB
+                                              : (unsigned)(wave * 32 * 144 + ((lane >> 3) + 8 * s4) * 144 + (lane & 7) * 16);
+                acc += *reinterpret_cast<const u32x4*>(lds + a);
+            }
+        }
+    }
+    asm volatile("" ::"v"(lds) : "memory");
+    if (acc.x == 0xdeadbeefu) sink[0] = acc.y;
+}
+
+// One wave: every lane reads (write = 0) or writes (write = 1) its linear slot of
+// `width` bytes (16 or 8), except lane `who`, which uses the slot of lane k moved by
+// `delta` bytes. Conflict cycles appear when that address shares a bank group, but not
+// the address, with a lane served in the same pass.
+__global__ __launch_bounds__(64) void lds_pair(unsigned* sink, int iters, int width, int write, int who, int k,
+                                               int delta) {
+    __shared__ __attribute__((aligned(1024))) unsigned char lds[65536];
+    const int lane = threadIdx.x;
+    for (int i = lane; i < 65536 / 16; i += 64) reinterpret_cast<u32x4*>(lds)[i] = u32x4{(unsigned)i, 1u, 2u, 3u};
+    __syncthreads();
+    const unsigned off = (unsigned)((lane == who ? k * width + delta : lane * width) & 32767);
+    u32x4 acc = {0u, 0u, 0u, 0u};
+    for (int it = 0; it < iters; ++it) {
+        asm volatile("" ::"v"(lds) : "memory");  // the stores are observable
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            unsigned char* p = lds + off + j * 4096;
+            if (width == 16 && !write) acc += *reinterpret_cast<const u32x4*>(p);
+            else if (width == 16) *reinterpret_cast<u32x4*>(p) = acc + (unsigned)it;
+            else if (!write) { const u32x2 v = *reinterpret_cast<const u32x2*>(p); acc.x += v.x; acc.y += v.y; }
+            else *reinterpret_cast<u32x2*>(p) = u32x2{acc.x + (unsigned)it, (unsigned)j};
+        }
+    }
+    asm volatile("" ::"v"(lds) : "memory");
+    if (acc.x == 0xdeadbeefu) sink[0] = acc.y;
+}
+
 }  // namespace
 
 extern "C" {
+
+// LDS bank probes; 0 on success, -1 on error. slime_probe_lds_pattern runs kind 0..6
+// of lds_pattern; slime_probe_lds_pair one displaced-lane pattern (width 16 or 8).
+int slime_probe_lds_pattern(int kind) {
+    unsigned* sink = nullptr;
+    if (hipMalloc(&sink, 4) != hipSuccess) return -1;
+    const dim3 g(256), b(256);
+    const int iters = 500;
+    switch (kind) {
+        case 0: hipLaunchKernelGGL(lds_pattern<0>, g, b, 0, 0, sink, iters); break;
+        case 1: hipLaunchKernelGGL(lds_pattern<1>, g, b, 0, 0, sink, iters); break;
+        case 2: hipLaunchKernelGGL(lds_pattern<2>, g, b, 0, 0, sink, iters); break;
+        case 3: hipLaunchKernelGGL(lds_pattern<3>, g, b, 0, 0, sink, iters); break;
+        case 4: hipLaunchKernelGGL(lds_pattern<4>, g, b, 0, 0, sink, iters); break;
+        case 5: hipLaunchKernelGGL(lds_pattern<5>, g, b, 0, 0, sink, iters); break;
+        case 6: hipLaunchKernelGGL(lds_pattern<6>, g, b, 0, 0, sink, iters); break;
+        default: (void)hipFree(sink); return -1;
+    }
+    const int rc = hipDeviceSynchronize() == hipSuccess ? 0 : -1;
+    (void)hipFree(sink);
+    return rc;
+}
+int slime_probe_lds_pair(int width, int write, int who, int k, int delta) {
+    if ((width != 8 && width != 16) || who < 0 || who > 63 || k < 0 || k > 63 || delta < 0 || delta > 16384) return -1;
+    unsigned* sink = nullptr;
+    if (hipMalloc(&sink, 4) != hipSuccess) return -1;
+    hipLaunchKernelGGL(lds_pair, dim3(1), dim3(64), 0, 0, sink, 100, width, write, who, k, delta);
+    const int rc = hipDeviceSynchronize() == hipSuccess ? 0 : -1;
+    (void)hipFree(sink);
+    return rc;
+}
+
 
 // Achieved bf16 MFMA rate in TFLOP/s of a 1024-workgroup run; random != 0 fills
 // the operands with finite bf16 values of magnitude < 2, else zeros. -1 on error.

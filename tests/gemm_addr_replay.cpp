@@ -12,6 +12,9 @@
 //     the wave's vector-memory operations (the direct loads and the epilogue's
 //     stores), and is exactly as tight as that (no looser, no stricter);
 //   * the bf16 epilogue's LDS staging stays inside the wave's own region;
+//   * the LDS layouts carry the data: each fragment read finds the tile row and
+//     16-byte chunk its MFMA needs, and each staged read-back the row and channels
+//     its global store writes (check_layouts);
 //   * each global store (and, for the adding epilogue, each addend load) lies
 //     inside its output plane;
 //   * the workgroups together visit every tile exactly once.
@@ -26,6 +29,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "../slime_amd/csrc/gemm_addr.hpp"
@@ -95,6 +99,76 @@ struct Wave {
     }
 };
 
+// The data path through the LDS layouts, independent of the tile: every 16-byte slot
+// of a stage is filled by exactly one direct-load lane, and each operand fragment read
+// finds there the tile row and logical 16-byte chunk of the slab that its MFMA needs;
+// every 8-byte slot of a wave's epilogue staging region is written by exactly one
+// (lane, piece), and each read-back (with its halves put back in order) holds the row
+// and chunk that its global store sends to that row and those channels.
+void check_layouts(long long row_bytes, long long ncol) {
+    struct Slot { int row = -1, chunk = -1; };
+    std::vector<Slot> stage(kStageB / 16);
+    for (int wave = 0; wave < kWaves; ++wave)
+        for (int j = 0; j < kDmaPerSlab; ++j)
+            for (int lane = 0; lane < 64; ++lane) {
+                const long long src = dma_grp_off(j, wave, row_bytes) + dma_lane_off(wave, lane, row_bytes);
+                const long long b = dma_lds_off(j, wave) + 16LL * lane;
+                in_range("direct-load destination inside the stage", b, 16, kStageB);
+                Slot& sl = stage[b / 16];
+                if (sl.row >= 0) fail("stage slot filled twice", b, wave, lane);
+                sl.row = (int)(src / row_bytes) + (j < 4 ? 0 : kBM);
+                sl.chunk = (int)((src % row_bytes) / 16);
+                if (src % 16 || sl.chunk >= kSlabB / 16) fail("direct-load source off a 16-byte chunk of the slab", src, wave, lane);
+            }
+    for (size_t i = 0; i < stage.size(); ++i)
+        if (stage[i].row < 0) fail("stage slot never filled", (long long)i, 0, 0);
+    for (int wave = 0; wave < kWaves; ++wave)
+        for (int lane = 0; lane < 64; ++lane)
+            for (int kk = 0; kk < 2; ++kk)
+                for (int q = 0; q < 4; ++q) {
+                    const int r32 = lane & 31, chunk = 2 * kk + (lane >> 5);
+#ifdef PLANT_FRAG_CHUNK  // a planted mistake: the cell fragment reads its chunk's neighbour
+                    const Slot& x = stage[((frag_x_off(kk, lane, wave) ^ 16u) + frag_block_off(q)) / 16];
+#else
+                    const Slot& x = stage[(frag_x_off(kk, lane, wave) + frag_block_off(q)) / 16];
+#endif
+                    if (x.row != r32 + 32 * q + 128 * (wave & 1) || x.chunk != chunk)
+                        fail("cell fragment reads the wrong row or chunk", lane, kk, q);
+                    const Slot& w = stage[(frag_w_off(kk, lane, wave) + frag_block_off(q)) / 16];
+                    if (w.row != kBM + r32 + 32 * q + 128 * (wave >> 1) || w.chunk != chunk)
+                        fail("weight fragment reads the wrong row or chunk", lane, kk, q);
+                }
+    struct Piece { int row = -1, chunk = -1, half = -1; };
+    for (int wave = 0; wave < kWaves; ++wave) {
+        std::vector<Piece> epi(kEpiWaveB / 8);
+        for (int lane = 0; lane < 64; ++lane)
+            for (int k = 0; k < 8; ++k) {
+                const long long b = (long long)epi_w_piece(epi_w_off(wave, lane), k) - wave * kEpiWaveB;
+                in_range("staging write inside the wave's region", b, 8, kEpiWaveB);
+                Piece& pc = epi[b / 8];
+                if (pc.row >= 0) fail("staging slot written twice", b, lane, k);
+                pc = {lane & 31, k, lane >> 5};
+            }
+        for (int lane = 0; lane < 64; ++lane)
+            for (int s4 = 0; s4 < 4; ++s4) {
+                const long long b = (long long)epi_r_off(wave, lane) + s4 * 8 * kEpiRowB - wave * kEpiWaveB;
+                in_range("staging read inside the wave's region", b, 16, kEpiWaveB);
+                Piece lo = epi[b / 8], hi = epi[b / 8 + 1];
+#ifndef PLANT_NO_UNSWAP  // a planted mistake: the read-back halves left as stored
+                if (epi_r_swapped(s4)) std::swap(lo, hi);
+#endif
+                const int R = lane / 8 + 8 * s4, c = lane & 7;
+                if (lo.row != R || hi.row != R || lo.chunk != c || hi.chunk != c || lo.half != 0 || hi.half != 1)
+                    fail("staging read-back holds the wrong row, chunk or half", lane, s4, wave);
+                for (int gr = 0; gr < 8; ++gr) {
+                    const long long o = bf16_store_off(gr, s4, (int)ncol) + epi_gl_off(lane, (int)ncol);
+                    const long long want = ((32LL * (gr >> 1) + R) * ncol + 64 * (gr & 1) + 8 * c) * 2;
+                    if (o != want) fail("bf16 store of a read-back goes to the wrong row or channels", lane, s4, gr);
+                }
+            }
+    }
+}
+
 void replay(const Launch& L) {
     const bool bf16_out = L.epi == "bf16";
     const bool add = L.epi == "f32add";
@@ -109,6 +183,7 @@ void replay(const Launch& L) {
     const int ntiles = (int)(L.M / kBM) * nN;
     if (L.M % kBM || L.N % kBN || L.ncol % kBN || nk % 4 || L.rows_per_batch % kBM || L.N > L.ncol * L.nplanes)
         fail("shape outside the MFMA kernel's domain", L.M, L.N, L.K);
+    check_layouts(row_bytes, L.ncol);
     const int grid = grid_size(ntiles, (int)L.n_cu);
     std::vector<int> visits(ntiles, 0);
     const int y_store = kStores + 2 * kDmaPerSlab <= 63 ? kStores + 2 * kDmaPerSlab : 0;
@@ -162,11 +237,10 @@ void replay(const Launch& L) {
             long long omin = 1LL << 62, omax = -(1LL << 62);
             for (int lane = 0; lane < 64; ++lane) {
                 if (bf16_out) {
-                    for (int ii = 0; ii < 2; ++ii)
-                        for (int q = 0; q < 4; ++q) {
-                            const long long w = epi_w_off(wave, lane) + (ii * 32 + 8 * q) * 2;
-                            in_range("epilogue staging write in the wave's region", w - wave * kEpiWaveB, 8, kEpiWaveB);
-                        }
+                    for (int k = 0; k < 8; ++k) {
+                        const long long w = epi_w_piece(epi_w_off(wave, lane), k);
+                        in_range("epilogue staging write in the wave's region", w - wave * kEpiWaveB, 8, kEpiWaveB);
+                    }
                     for (int s4 = 0; s4 < 4; ++s4)
                         in_range("epilogue staging read in the wave's region",
                                  epi_r_off(wave, lane) + s4 * 8 * kEpiRowB - wave * kEpiWaveB, 16, kEpiWaveB);

@@ -90,3 +90,16 @@ def test_replay_reports_planted_mistakes(replay):
     assert rc == 1 and "direct load from Bt" in out, out
     rc, out = _run(replay, args, 256, ("plant-loose-wait",))
     assert rc == 1 and "too loose" in out, out
+
+
+@pytest.mark.parametrize("plant,message", [
+    ("PLANT_FRAG_CHUNK", "cell fragment reads the wrong row or chunk"),
+    ("PLANT_NO_UNSWAP", "staging read-back holds the wrong row, chunk or half"),
+])
+def test_layout_check_reports_planted_mistakes(tmp_path, plant, message):
+    """The LDS data-path check fires when a fragment read takes the neighbouring
+    16-byte chunk, or when the staged read-back keeps its rows' halves swapped."""
+    exe = str(tmp_path / "replay_planted")
+    subprocess.run(["g++", "-O2", "-std=c++17", f"-D{plant}", "-o", exe, SRC], check=True)
+    rc, out = _run(exe, next(launches(CONFIGS["c3"])), 256)
+    assert rc == 1 and message in out, out
