@@ -36,7 +36,7 @@ struct slime_ca {
     float* mu = nullptr;       // [pods][H] or [pods][G][G][H]
     float* sigma = nullptr;
     float* M = nullptr;        // [pods][H][H]
-    void* kmat = nullptr;      // bf16, D = 64: the stencil's K matrices (fill_stencil_kmat)
+    void* kband = nullptr;     // bf16, D = 64: the stencil's 3x3 band table (fill_stencil_kband)
     void* P = nullptr;         // [B][G][G][C] work buffers for slime_ca_step
     void* I = nullptr;
     void* V = nullptr;
@@ -180,7 +180,7 @@ hipError_t timed(slime_ca* h, std::vector<std::pair<size_t, size_t>>& log, hipSt
 void release(slime_ca* h) {
     for (hipEvent_t e : h->ev_pool) (void)hipEventDestroy(e);
     h->ev_pool.clear();
-    void* ptrs[] = {h->Wtm, h->Wt, h->K, h->mu, h->sigma, h->M, h->kmat, h->P, h->I, h->V, h->S[0], h->S[1], h->Sf,
+    void* ptrs[] = {h->Wtm, h->Wt, h->K, h->mu, h->sigma, h->M, h->kband, h->P, h->I, h->V, h->S[0], h->S[1], h->Sf,
                     h->part_in, h->part_out, h->scale[0], h->scale[1], h->unit_scale,
                     h->mass_in, h->mass_out, h->gram_part, h->mom_part, h->sweeps, h->org_fit,
                     h->Wcat, h->Ipre, h->bw_lpart, h->bw_coef, h->bw_loss, h->bw_gU, h->bw_gVt,
@@ -269,7 +269,7 @@ int run_stencil(slime_ca* h, const void* x, const float* x_scale, const void* P,
     a.mu = h->mu;
     a.sigma = h->sigma;
     a.M = h->M;
-    a.kmat = h->kmat;
+    a.kband = h->kband;
     a.part_in = h->part_in;
     a.part_out = h->part_out;
     a.B = c.B;
@@ -367,7 +367,7 @@ int slime_ca_create(const slime_ca_config* config, slime_ca** out) {
     rc = rc ? rc : dalloc_t(&h->mu, n_param_growth(c) * 4);
     rc = rc ? rc : dalloc_t(&h->sigma, n_param_growth(c) * 4);
     rc = rc ? rc : dalloc_t(&h->M, (size_t)c.pods * c.H * c.H * 4);
-    if (c.dtype == SLIME_BF16 && c.D == 64) rc = rc ? rc : dalloc(&h->kmat, stencil_kmat_bytes(c.pods));
+    if (c.dtype == SLIME_BF16 && c.D == 64) rc = rc ? rc : dalloc(&h->kband, stencil_kband_bytes(c.pods));
     rc = rc ? rc : dalloc(&h->P, state_bytes);
     rc = rc ? rc : dalloc(&h->I, state_bytes);
     rc = rc ? rc : dalloc(&h->V, state_bytes);
@@ -456,10 +456,10 @@ int slime_ca_set_params(slime_ca* h, const slime_ca_params* p) {
         h->Wcat = nullptr;
     }
     HIP_TRY(hipMemcpy(h->K, p->K, (size_t)c.pods * c.H * 9 * 4, hipMemcpyHostToDevice));
-    if (h->kmat) {
-        std::vector<uint16_t> km(stencil_kmat_bytes(c.pods) / 2);
-        fill_stencil_kmat(p->K, c.pods, km.data());
-        HIP_TRY(hipMemcpy(h->kmat, km.data(), km.size() * 2, hipMemcpyHostToDevice));
+    if (h->kband) {
+        std::vector<uint32_t> kb(stencil_kband_bytes(c.pods) / 4);
+        fill_stencil_kband(p->K, c.pods, kb.data());
+        HIP_TRY(hipMemcpy(h->kband, kb.data(), kb.size() * 4, hipMemcpyHostToDevice));
     }
     HIP_TRY(hipMemcpy(h->mu, p->mu, ng * 4, hipMemcpyHostToDevice));
     HIP_TRY(hipMemcpy(h->sigma, p->sigma, ng * 4, hipMemcpyHostToDevice));

@@ -58,20 +58,20 @@ struct StencilArgs {
     const float* mu;         // [pods][H] or [pods][G][G][H]
     const float* sigma;
     const float* M;          // [pods][H][H]
-    // bf16 state, D = 64 only: the potential's 9-tap weights as dense bf16 hi/lo
-    // matrices over a 4x8 tile's 6x10 halo, [pods][H][2][32 cells][64 halo rows]
-    // (stencil_kmat_bytes / fill_stencil_kmat).
-    const void* kmat;
+    // bf16 state, D = 64 only: the potential's 9-tap weights as a band table,
+    // [pods][H][3 kernel rows][A_hi, B_hi, A_lo, B_lo] with A = bf16 K[3r] | K[3r+1] << 16
+    // and B = K[3r+2] (stencil_kband_bytes / fill_stencil_kband, stencil_band.hpp).
+    const void* kband;
     double* part_in;         // [B][H][tiles]  sum of scaled X per tile
     double* part_out;        // [B][H][tiles]  sum of stored Y per tile
     int B, G, D, per_pod, per_cell;
     float dt;
 };
 int stencil_tiles_per_batch(int G);
-// Host-side table for StencilArgs::kmat: bytes for `pods` pods, and its contents
-// from K [pods][H][9] (fp32).
-size_t stencil_kmat_bytes(int pods);
-void fill_stencil_kmat(const float* K, int pods, uint16_t* out);
+// Host-side table for StencilArgs::kband: bytes for `pods` pods, and its contents
+// from K [pods][H][9] (fp32), each weight split into bf16 hi + lo.
+size_t stencil_kband_bytes(int pods);
+void fill_stencil_kband(const float* K, int pods, uint32_t* out);
 hipError_t launch_stencil(int dtype, const StencilArgs& a, hipStream_t s);
 
 // ---- S7 mass conservation ------------------------------------------------------------

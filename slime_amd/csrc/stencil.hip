@@ -25,6 +25,7 @@
 // reductions, then a cross-wave pass through LDS).
 #include "common.hpp"
 #include "kernels.hpp"
+#include "stencil_band.hpp"
 
 #include <cstring>
 #include <type_traits>
@@ -490,8 +491,10 @@ __global__ __launch_bounds__((Layout<T, D>::kThreads), 2) void stencil_kernel(St
 // are bf16 already, so every product is exact in fp32 and the sums keep fp32
 // accuracy. The halo^T operands come straight from the row-major halo through
 // ds_read_b64_tr_b16 (gfx950's transposing LDS read). Kmat depends only on the
-// pod, the head and the tile geometry, so it is built once on the host
-// (fill_stencil_kmat) and read from L2; Att is built per head.
+// pod's 9 weights of the head and the tile geometry: each lane builds its Kmat^T
+// operand with v_perm_b32 from a 12-dword table per (pod, head) that sits in the
+// tile's parameter block (stencil_band.hpp), so the weights cost no vector-memory
+// traffic; Att is built per head.
 //
 // Work split: wave w owns cell block cb = w/2 (tile rows 2cb, 2cb+1: 16 cells)
 // and channel half w%2 (32 channels). Each wave computes the scores <P, I> of its
@@ -517,11 +520,14 @@ constexpr int kBufB = (3 * kHaloPad + kTileCells) * kRowB;  // 28 KiB
 constexpr int kWC = 16;                                     // cells per wave
 constexpr int kAttB = kWC * kRowB;                          // one 16 x 64 bf16 matrix
 constexpr int kS9 = 12;  // floats per cell in a score buffer (9 used, 9..11 take discards)
-constexpr int kKmatHead = 2 * kTileCells * kRowB;           // hi + lo, 8 KiB per (pod, head)
 // Per-tile parameter block (fp32): M[8][8] (M[o][h] at o*8+h), mu[8], sigma[8],
-// scale[8] and its low part[8]; then, for per-cell growth, mu and sigma [cell][8].
+// scale[8] and its low part[8]; then, for per-cell growth, mu and sigma [cell][8];
+// then the pod's 3x3-kernel band table (stencil_band.hpp), 12 dwords per head.
 constexpr int kPM = 0, kPMu = 64, kPSg = 72, kPSc = 80, kPScLo = 88, kPScal = 96;
-constexpr int kPCellMu = 96, kPCellSg = 96 + kTileCells * 8, kParF = 96 + 2 * kTileCells * 8;
+constexpr int kPCellMu = 96, kPCellSg = 96 + kTileCells * 8, kPBand = 96 + 2 * kTileCells * 8;
+constexpr int kBandHead = 12;                       // dwords per head: 3 runs x {A, B} x {hi, lo}
+constexpr int kParF = kPBand + kHeads * kBandHead;
+static_assert(kPBand % 4 == 0, "band table rows are read as 16-byte vectors");
 
 // 16-byte chunk swizzles inside a 128-byte row. X and V: any four consecutive
 // rows 4j..4j+3, and rows {r, r+2, r+8, r+10}, occupy disjoint chunk pairs, so
@@ -615,16 +621,14 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
     const int cb = wave >> 1, chh = wave & 1;   // cell block, channel half
     const int grp = lane >> 4, i16 = lane & 15;
     const int cell = kWC * cb + i16;            // this lane's cell in phase B
-    const char* kmat = static_cast<const char*>(a.kmat);
+    const unsigned* kband = static_cast<const unsigned*>(a.kband);
 
     // ---- staging: 8 halo rows (or P rows) per direct-load instruction -------------------
     // Lane l of an instruction lands at row g*8 + l/8, physical chunk l%8, and fetches
     // the logical chunk the row's swizzle maps there. Wave w issues groups w and w+4
-    // of each halo array and group w of the P tile. With the staging, each lane
-    // fetches its Kmat operands (cell, halo rows 32 ks + 8 grp .. +7, hi and lo).
+    // of each halo array and group w of the P tile.
     unsigned boff_xv[2], boff_i[2], boff_p;
     const char *srcX, *srcV, *srcI, *srcP;
-    int pod_nxt = 0;
     auto set_tile = [&](int t) {  // per-lane offsets and bases of tile t
         const int b = t / tpb, tile = t % tpb;
         const int ty0 = (tile / tiles_x) * kTileY, tx0 = (tile % tiles_x) * kTileX;
@@ -646,9 +650,7 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
         srcV = reinterpret_cast<const char*>(static_cast<const bf16_t*>(a.V) + bb);
         srcI = reinterpret_cast<const char*>(static_cast<const bf16_t*>(a.I) + bb);
         srcP = reinterpret_cast<const char*>(static_cast<const bf16_t*>(a.P) + bb);
-        pod_nxt = b / a.per_pod;
     };
-    uint4 kq[2][2], kq_nxt[2][2];  // Kmat^T operands [ks][hi/lo]
     auto issue_head = [&](int h, unsigned char* buf) {
         const unsigned hb = (unsigned)(h * kRowB);
         const unsigned lb = lds_addr(buf);
@@ -660,20 +662,16 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
             dma16_saddr(srcI, boff_i[k] + hb, row + offI);
         }
         dma16_saddr(srcP, boff_p + hb, lb + offP + wave * 1024);
-        const char* km = kmat + (long long)(pod_nxt * H + h) * kKmatHead + cell * kRowB + 16 * grp;
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-            for (int m = 0; m < 2; ++m)
-                kq_nxt[ks][m] = *reinterpret_cast<const uint4*>(km + m * (kTileCells * kRowB) + 64 * ks);
     };
-    // Per-tile parameters: up to three floats per lane, loaded into registers with
+    // Per-tile parameters: up to four values per lane, loaded into registers with
     // the tile's first staging and written to LDS once they have landed.
     float pre[3];
+    unsigned pre_band = 0u;
     auto fetch_params = [&](int t) {
         const int b = t / tpb, tile = t % tpb;
         const int pod = b / a.per_pod;
         pre[0] = pre[1] = pre[2] = 0.f;
+        if (tid < H * kBandHead) pre_band = kband[pod * H * kBandHead + tid];
         if (tid < kPM + 64) pre[0] = a.M[pod * 64 + tid - kPM];
         else if (tid < kPSg + 8) {
             if (!a.per_cell) pre[0] = tid < kPSg ? a.mu[pod * 8 + tid - kPMu] : a.sigma[pod * 8 + tid - kPSg];
@@ -693,6 +691,7 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
     };
     auto store_params = [&](float* par) {
         if (tid < kPScal) par[tid] = pre[0];
+        if (tid < H * kBandHead) reinterpret_cast<unsigned*>(par)[kPBand + tid] = pre_band;
         if (a.per_cell) {
             par[kPCellMu + tid] = pre[1];
             par[kPCellSg + tid] = pre[2];
@@ -766,6 +765,15 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
         }
     }
     const int ch0 = 32 * chh + 4 * grp;  // + 16 mb: this lane's output channels
+    // Kmat^T operand of this lane (cell, halo rows 32 ks + 8 grp .. +7): the band-table
+    // run it meets (dword offset in a head's table) and the byte selectors of its dwords.
+    unsigned band_row[2], band_sel[2][4];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+        band_row[ks] = (unsigned)(4 * band::band_run(cell, grp, ks));
+#pragma unroll
+        for (int d = 0; d < 4; ++d) band_sel[ks][d] = band::band_sel(cell, grp, ks, d);
+    }
 
     constexpr float kLog2e = 1.4426950408889634f;
     const float score_scale = kLog2e / 8.0f;  // log2(e) / sqrt(D)
@@ -795,10 +803,6 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
             unsigned char* nxt = (gh & 1) ? bufA : bufB;
             wait_vm0();       // this wave's loads of head h have landed
             __syncthreads();  // ... and every other wave's; head h-1 is fully consumed
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-                for (int m = 0; m < 2; ++m) kq[ks][m] = kq_nxt[ks][m];
             if (h == 0) store_params(par);
             if (h + 1 < H) {
                 issue_head(h + 1, nxt);
@@ -855,6 +859,22 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
 #pragma unroll
                     for (int m = 0; m < 2; ++m)
                         aw[ks][m] = *reinterpret_cast<const uint4*>(att + m * kAttB + at_off[ks]);
+                uint4 kq[2][2];  // Kmat^T [ks][hi/lo], from the head's band-table run
+                {
+                    const unsigned* kb = reinterpret_cast<const unsigned*>(par) + kPBand + h * kBandHead;
+#pragma unroll
+                    for (int ks = 0; ks < 2; ++ks) {
+                        const uint4 t = *reinterpret_cast<const uint4*>(kb + band_row[ks]);  // A, B hi; A, B lo
+                        kq[ks][0] = make_uint4(__builtin_amdgcn_perm(t.y, t.x, band_sel[ks][0]),
+                                               __builtin_amdgcn_perm(t.y, t.x, band_sel[ks][1]),
+                                               __builtin_amdgcn_perm(t.y, t.x, band_sel[ks][2]),
+                                               __builtin_amdgcn_perm(t.y, t.x, band_sel[ks][3]));
+                        kq[ks][1] = make_uint4(__builtin_amdgcn_perm(t.w, t.z, band_sel[ks][0]),
+                                               __builtin_amdgcn_perm(t.w, t.z, band_sel[ks][1]),
+                                               __builtin_amdgcn_perm(t.w, t.z, band_sel[ks][2]),
+                                               __builtin_amdgcn_perm(t.w, t.z, band_sel[ks][3]));
+                    }
+                }
                 f32x4 u[2], vt[2];
 #pragma unroll
                 for (int mb = 0; mb < 2; ++mb) {
@@ -1004,7 +1024,7 @@ hipError_t launch_t(const StencilArgs& a, hipStream_t s) {
 
 int stencil_tiles_per_batch(int G) { return (G / kTileY) * (G / kTileX); }
 
-size_t stencil_kmat_bytes(int pods) { return (size_t)pods * kHeads * mf::kKmatHead; }
+size_t stencil_kband_bytes(int pods) { return (size_t)pods * kHeads * mf::kBandHead * 4; }
 
 namespace {
 // fp32 -> bf16 bits, round to nearest even (finite inputs).
@@ -1022,21 +1042,21 @@ float host_f32(uint16_t b) {
 }
 }  // namespace
 
-void fill_stencil_kmat(const float* K, int pods, uint16_t* out) {
-    constexpr int kRow = mf::kD;  // halo rows per cell row (64)
-    std::memset(out, 0, stencil_kmat_bytes(pods));
+void fill_stencil_kband(const float* K, int pods, uint32_t* out) {
     for (int p = 0; p < pods; ++p)
         for (int h = 0; h < kHeads; ++h) {
-            uint16_t* hi = out + (size_t)(p * kHeads + h) * (mf::kKmatHead / 2);
-            uint16_t* lo = hi + kTileCells * kRow;
-            for (int k = 0; k < 9; ++k) {
-                const float w = K[(p * kHeads + h) * 9 + k];
-                const uint16_t wh = host_bf16(w);
-                const uint16_t wl = host_bf16(w - host_f32(wh));
-                for (int c = 0; c < kTileCells; ++c) {
-                    hi[c * kRow + mf::nb_row(c, k)] = wh;
-                    lo[c * kRow + mf::nb_row(c, k)] = wl;
+            const float* k = K + (p * kHeads + h) * 9;
+            uint32_t* t = out + (size_t)(p * kHeads + h) * mf::kBandHead;
+            for (int r = 0; r < 3; ++r) {
+                uint16_t hi[3], lo[3];
+                for (int q = 0; q < 3; ++q) {
+                    hi[q] = host_bf16(k[3 * r + q]);
+                    lo[q] = host_bf16(k[3 * r + q] - host_f32(hi[q]));
                 }
+                t[4 * r + 0] = hi[0] | (uint32_t)hi[1] << 16;  // A_hi
+                t[4 * r + 1] = hi[2];                          // B_hi
+                t[4 * r + 2] = lo[0] | (uint32_t)lo[1] << 16;  // A_lo
+                t[4 * r + 3] = lo[2];                          // B_lo
             }
         }
 }
