@@ -932,7 +932,34 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
         float ysum[H];  // this lane's sum of stored Y per head
 #pragma unroll
         for (int o = 0; o < H; ++o) ysum[o] = 0.f;
-        {
+        if constexpr (sizeof(TY) == 2) {
+            // bf16: lanes grp and grp ^ 1 (lane ^ 16, the same cell) exchange one
+            // 8-byte piece per head so that each stores 8 contiguous channels in one
+            // 16-byte store -- even grp the mb = 0 block's, odd grp the mb = 1 block's
+            // -- halving the store instructions of the tile.
+            const bool odd = grp & 1;
+            const long long base = bbase + ((long long)(ty0 + cell / kTileX) * G + tx0 + cell % kTileX) * C +
+                                   32 * chh + 16 * (grp & 1) + 8 * (grp >> 1);
+#pragma unroll
+            for (int o = 0; o < H; ++o) {
+                uint2 pk[2];
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb) {
+                    float r[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        r[e] = Store<TY>::round(y[o][mb][e]);
+                        ysum[o] += r[e];
+                    }
+                    pk[mb] = make_uint2(pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3]));
+                }
+                const uint2 send = odd ? pk[0] : pk[1];
+                const uint2 recv = make_uint2(__shfl_xor(send.x, 16), __shfl_xor(send.y, 16));
+                const uint4 v = odd ? make_uint4(recv.x, recv.y, pk[1].x, pk[1].y)
+                                    : make_uint4(pk[0].x, pk[0].y, recv.x, recv.y);
+                *reinterpret_cast<uint4*>(Yg + base + o * kD) = v;
+            }
+        } else {
             const long long base =
                 bbase + ((long long)(ty0 + cell / kTileX) * G + tx0 + cell % kTileX) * C + ch0;
 #pragma unroll
@@ -945,13 +972,9 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
                         r[e] = Store<TY>::round(y[o][mb][e]);
                         ysum[o] += r[e];
                     }
-                    TY* dst = Yg + base + o * kD + 16 * mb;
-                    // 32-byte pieces per cell: plain stores, so L2 merges the pieces of
-                    // each 128-byte line before it is written back.
-                    if constexpr (sizeof(TY) == 2)
-                        *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3]));
-                    else
-                        *reinterpret_cast<float4*>(dst) = make_float4(r[0], r[1], r[2], r[3]);
+                    // fp32: 16-byte pieces per cell, plain stores, so L2 merges the
+                    // pieces of each 128-byte line before it is written back.
+                    *reinterpret_cast<float4*>(Yg + base + o * kD + 16 * mb) = make_float4(r[0], r[1], r[2], r[3]);
                 }
         }
         // Wave sums of the 16 values: the butterfly leaves lane l holding its 16-lane
