@@ -37,6 +37,7 @@ struct slime_ca {
     float* sigma = nullptr;
     float* M = nullptr;        // [pods][H][H]
     void* kband = nullptr;     // bf16, D = 64: the stencil's 3x3 band table (fill_stencil_kband)
+    unsigned* sched = nullptr;  // bf16, D = 64: the stencil's 16 tile counters (StencilArgs::sched)
     void* P = nullptr;         // [B][G][G][C] work buffers for slime_ca_step
     void* I = nullptr;
     void* V = nullptr;
@@ -180,8 +181,8 @@ hipError_t timed(slime_ca* h, std::vector<std::pair<size_t, size_t>>& log, hipSt
 void release(slime_ca* h) {
     for (hipEvent_t e : h->ev_pool) (void)hipEventDestroy(e);
     h->ev_pool.clear();
-    void* ptrs[] = {h->Wtm, h->Wt, h->K, h->mu, h->sigma, h->M, h->kband, h->P, h->I, h->V, h->S[0], h->S[1], h->Sf,
-                    h->part_in, h->part_out, h->scale[0], h->scale[1], h->unit_scale,
+    void* ptrs[] = {h->Wtm, h->Wt, h->K, h->mu, h->sigma, h->M, h->kband, h->sched, h->P, h->I, h->V,
+                    h->S[0], h->S[1], h->Sf, h->part_in, h->part_out, h->scale[0], h->scale[1], h->unit_scale,
                     h->mass_in, h->mass_out, h->gram_part, h->mom_part, h->sweeps, h->org_fit,
                     h->Wcat, h->Ipre, h->bw_lpart, h->bw_coef, h->bw_loss, h->bw_gU, h->bw_gVt,
                     h->bw_att, h->bw_gS, h->bw_G3, h->bw_gXd, h->bw_ppart, h->bw_gcell, h->bw_gXp,
@@ -270,6 +271,7 @@ int run_stencil(slime_ca* h, const void* x, const float* x_scale, const void* P,
     a.sigma = h->sigma;
     a.M = h->M;
     a.kband = h->kband;
+    a.sched = h->sched;
     a.part_in = h->part_in;
     a.part_out = h->part_out;
     a.B = c.B;
@@ -367,7 +369,10 @@ int slime_ca_create(const slime_ca_config* config, slime_ca** out) {
     rc = rc ? rc : dalloc_t(&h->mu, n_param_growth(c) * 4);
     rc = rc ? rc : dalloc_t(&h->sigma, n_param_growth(c) * 4);
     rc = rc ? rc : dalloc_t(&h->M, (size_t)c.pods * c.H * c.H * 4);
-    if (c.dtype == SLIME_BF16 && c.D == 64) rc = rc ? rc : dalloc(&h->kband, stencil_kband_bytes(c.pods));
+    if (c.dtype == SLIME_BF16 && c.D == 64) {
+        rc = rc ? rc : dalloc(&h->kband, stencil_kband_bytes(c.pods));
+        rc = rc ? rc : dalloc_t(&h->sched, 16 * sizeof(unsigned));
+    }
     rc = rc ? rc : dalloc(&h->P, state_bytes);
     rc = rc ? rc : dalloc(&h->I, state_bytes);
     rc = rc ? rc : dalloc(&h->V, state_bytes);
@@ -394,6 +399,7 @@ int slime_ca_create(const slime_ca_config* config, slime_ca** out) {
     delete[] ones;
     if (e == hipSuccess) e = hipMemset(h->mass_in, 0, BH * 8);
     if (e == hipSuccess) e = hipMemset(h->mass_out, 0, BH * 8);
+    if (e == hipSuccess && h->sched) e = hipMemset(h->sched, 0, 16 * sizeof(unsigned));
     if (e != hipSuccess) {
         release(h);
         delete h;

@@ -62,6 +62,10 @@ struct StencilArgs {
     // [pods][H][3 kernel rows][A_hi, B_hi, A_lo, B_lo] with A = bf16 K[3r] | K[3r+1] << 16
     // and B = K[3r+2] (stencil_kband_bytes / fill_stencil_kband, stencil_band.hpp).
     const void* kband;
+    // bf16 state, D = 64 only: 16 counters (tile tickets per XCD, then finished
+    // workgroups per XCD), zero before a launch; each launch leaves them zero. Launches
+    // that share them must be stream-ordered.
+    unsigned* sched;
     double* part_in;         // [B][H][tiles]  sum of scaled X per tile
     double* part_out;        // [B][H][tiles]  sum of stored Y per tile
     int B, G, D, per_pod, per_cell;

@@ -210,6 +210,33 @@ def test_persistent_tiles_across_batches_and_pods(oracle):
     np.testing.assert_allclose(mo, mi, rtol=1e-6)
 
 
+def test_tile_tickets_cover_every_tile_on_each_launch(oracle):
+    # After its fixed first tiles a workgroup draws its tiles from a per-XCD ticket
+    # counter that the launch leaves at zero for the next one. Three launches on one
+    # handle with three different states: a launch that skipped tiles would leave the
+    # previous launch's values in the handle's output buffer, so each result is
+    # checked in full against the oracle for its own state.
+    cfg = _cfg("tickets", B=24, G=32, D=64, dtype="bf16", pods=3)
+    p = _prep(cfg)[0]
+    ocfg = _ocfg(cfg)
+    with _engine(cfg) as e:
+        e.set_params(p)
+        for seed in (2, 3, 4):
+            X = round_bf16(make_state(cfg, seed=seed))
+            x = _dev(X, "bf16")
+            P, I, V = e.project(x)
+            y = e.flow_lenia(x, P, I, V)
+            torch.cuda.synchronize()
+            mi, mo = e.mass()
+            hp, hi, hv, Y = (_host(t) for t in (P, I, V, y))
+            ref, rmi, _ = _oracle_flow(oracle, ocfg, X, hp, hi, hv, p)
+            errs = [norm_err(Y[b], ref[b]) for b in range(cfg.B)]
+            print(f"  launch with state seed {seed}: max normalised error over batches {max(errs):.3e}")
+            assert max(errs) <= TOL["bf16"], (seed, int(np.argmax(errs)), max(errs))
+            np.testing.assert_allclose(mi, rmi, rtol=1e-6)
+            np.testing.assert_allclose(mo, mi, rtol=1e-6)
+
+
 def test_multi_step_bf16_conserves_mass_and_tracks_oracle(oracle):
     # Two steps in one call: the second folds the first step's mass scale into its
     # weights and X loads; mass is conserved against the caller's input.
