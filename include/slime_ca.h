@@ -186,6 +186,16 @@ int slime_ca_fitness_sweeps(slime_ca* ca, int* h_sweeps);
 int slime_ca_init_from_field(slime_ca* ca, const float* conc, void* x, void* stream);
 int slime_ca_field_from_state(slime_ca* ca, const void* x, float* conc, void* stream);
 
+/* Read-back for visualisation; replaces get_ca_state (slime/runtime.cu:479-504, with
+ * extract_ca_channel_kernel :506-518), which copies `size` floats of the organism's
+ * chemical concentration to the host. After a generation that field is
+ * update_field_from_ca of the CA output, so this computes conc = mean_c X of the
+ * device state `x` (one G x G grid, handle dtype) and copies its first `size` values
+ * (row-major, 0 <= size <= G*G, else SLIME_EINVAL) to the host array h_buffer.
+ * Synchronous like the reference: it waits for all work on the device, so `x` may
+ * come from any stream. */
+int slime_ca_get_state(slime_ca* ca, const void* x, float* h_buffer, int size);
+
 /* The buffers of the reference's MultiHeadCAState (slime/core/pseudopod.cu:29-38)
  * that one organism generation reads and writes, under the same field names. The
  * parameter fields of that struct (perception_weights, interaction_weights,

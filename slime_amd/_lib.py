@@ -24,6 +24,7 @@ EXPORTS = (
     "slime_ca_create", "slime_ca_destroy", "slime_ca_set_params", "slime_ca_project",
     "slime_ca_flow_lenia", "slime_ca_step", "slime_ca_mass", "slime_ca_fitness",
     "slime_ca_fitness_sweeps", "slime_ca_init_from_field", "slime_ca_field_from_state",
+    "slime_ca_get_state",
     "slime_ca_uses_mfma", "slime_ca_set_timing", "slime_ca_timings", "slime_ca_last_error",
     "slime_neural_ca_update", "slime_ca_backward", "slime_pool_init", "slime_pool_set_fitness",
     "slime_ca_hunger", "slime_pool_age", "slime_pool_cull", "slime_pool_spawn", "slime_pool_spawn_wave",
@@ -91,6 +92,7 @@ def load() -> ctypes.CDLL:
         "slime_ca_fitness_sweeps": [vp, vp],
         "slime_ca_init_from_field": [vp, vp, vp, vp],
         "slime_ca_field_from_state": [vp, vp, vp, vp],
+        "slime_ca_get_state": [vp, vp, vp, i],
         "slime_ca_uses_mfma": [vp],
         "slime_ca_set_timing": [vp, i],
         "slime_ca_timings": [vp, vp, vp, vp, vp],

@@ -292,3 +292,11 @@ class Pseudopod:
         conc = torch.empty((self.G, self.G), dtype=torch.float32, device="cuda")
         _lib.check(self.lib.slime_ca_field_from_state(self._h, _ptr(x), _ptr(conc), _stream(stream)))
         return conc
+
+    def get_state(self, x, size=None):
+        """The field of state ``x`` on the host (get_ca_state, slime/runtime.cu:479-504):
+        the first ``size`` (default G*G) values of mean_c x, row-major, as float32."""
+        n = self.G * self.G if size is None else int(size)
+        out = np.empty(max(n, 0), dtype=np.float32)
+        _lib.check(self.lib.slime_ca_get_state(self._h, _ptr(x), out.ctypes.data, n))
+        return out

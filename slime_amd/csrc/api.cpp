@@ -56,6 +56,7 @@ struct slime_ca {
     double* mom_part = nullptr;
     int* sweeps = nullptr;     // [B*H]
     float* org_fit = nullptr;  // [3][B*H] erank, coherence, fitness of slime_neural_ca_update
+    float* view = nullptr;     // [G][G] field of slime_ca_get_state (allocated on its first call)
 
     // slime_ca_backward (allocated on its first call)
     void* Wcat = nullptr;      // [pods][C][3C] = [W_P | W_I | W_V] row k (input channel), dtype
@@ -183,7 +184,7 @@ void release(slime_ca* h) {
     h->ev_pool.clear();
     void* ptrs[] = {h->Wtm, h->Wt, h->K, h->mu, h->sigma, h->M, h->kband, h->sched, h->P, h->I, h->V,
                     h->S[0], h->S[1], h->Sf, h->part_in, h->part_out, h->scale[0], h->scale[1], h->unit_scale,
-                    h->mass_in, h->mass_out, h->gram_part, h->mom_part, h->sweeps, h->org_fit,
+                    h->mass_in, h->mass_out, h->gram_part, h->mom_part, h->sweeps, h->org_fit, h->view,
                     h->Wcat, h->Ipre, h->bw_lpart, h->bw_coef, h->bw_loss, h->bw_gU, h->bw_gVt,
                     h->bw_att, h->bw_gS, h->bw_G3, h->bw_gXd, h->bw_ppart, h->bw_gcell, h->bw_gXp,
                     h->bw_dwpart, h->bw_y32};
@@ -672,6 +673,24 @@ int slime_ca_field_from_state(slime_ca* h, const void* x, float* conc, void* str
     hipStream_t s = static_cast<hipStream_t>(stream);
     h->last_stream = s;
     HIP_TRY(launch_field_from_state(h->cfg.dtype, x, conc, h->cfg.G, h->C, s));
+    return SLIME_OK;
+}
+
+int slime_ca_get_state(slime_ca* h, const void* x, float* h_buffer, int size) {
+    int rc = use_handle(h);
+    if (rc) return rc;
+    if (!x || !h_buffer) return fail(SLIME_EINVAL, "a pointer is NULL");
+    const long long cells = (long long)h->cfg.G * h->cfg.G;
+    if (size < 0 || size > cells)
+        return fail(SLIME_EINVAL, "size=%d is outside [0, G*G = %lld]", size, cells);
+    if (size == 0) return SLIME_OK;
+    if (!h->view) {
+        rc = dalloc_t(&h->view, (size_t)cells * 4);
+        if (rc) return rc;
+    }
+    HIP_TRY(hipDeviceSynchronize());
+    HIP_TRY(launch_field_from_state(h->cfg.dtype, x, h->view, h->cfg.G, h->C, nullptr));
+    HIP_TRY(hipMemcpy(h_buffer, h->view, (size_t)size * 4, hipMemcpyDeviceToHost));
     return SLIME_OK;
 }
 

@@ -88,6 +88,7 @@ def test_null_arguments_are_errors_not_crashes():
     assert lib.slime_ca_destroy(None) == _lib.SLIME_OK
     assert lib.slime_ca_uses_mfma(None) == 0
     assert lib.slime_neural_ca_update(None, None, None, None, 0, None) == _lib.SLIME_EINVAL
+    assert lib.slime_ca_get_state(None, None, None, 16) == _lib.SLIME_EINVAL
     assert b"NULL" in lib.slime_ca_last_error()
 
 

@@ -423,6 +423,31 @@ def test_field_adapters_match_oracle(oracle):
     assert np.max(np.abs(C2 - oracle.field_from_state(ref)) / scale) <= 1e-6
 
 
+@pytest.mark.parametrize("dtype", ["fp32", "bf16"])
+def test_get_state_reads_back_the_field_of_a_state(oracle, dtype):
+    # get_ca_state (slime/runtime.cu:479-504) copies the organism's concentration,
+    # which after a generation is mean_c of the CA output (organism.cu:723-743).
+    cfg = _cfg("view", B=1, G=32, D=64, dtype=dtype)
+    p, X = _prep(cfg)
+    with _engine(cfg) as e:
+        e.set_params(p)
+        y = e.forward(_dev(X, dtype))  # on torch's stream; get_state waits for the device
+        full = e.get_state(y)
+        part = e.get_state(y, size=100)
+        none = e.get_state(y, size=0)
+        conc = _host(e.field_from_state(y))
+        Y = _host(y)
+        with pytest.raises(Exception):
+            e.get_state(y, size=cfg.G * cfg.G + 1)
+        with pytest.raises(Exception):
+            e.get_state(y, size=-1)
+    assert full.shape == (cfg.G * cfg.G,) and part.shape == (100,) and none.shape == (0,)
+    np.testing.assert_array_equal(full, conc.reshape(-1))
+    np.testing.assert_array_equal(part, full[:100])
+    ref = oracle.field_from_state(Y[0]).reshape(-1)
+    assert np.max(np.abs(full - ref)) <= 1e-6 * np.max(np.abs(ref))
+
+
 @pytest.mark.parametrize("D", [8, 64])
 def test_neural_ca_update_matches_oracle_organism_sequence(oracle, D):
     """slime_neural_ca_update = init-from-field -> one step -> field update -> mean
