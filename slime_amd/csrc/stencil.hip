@@ -960,8 +960,11 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
             // bf16: lanes grp and grp ^ 1 (lane ^ 16, the same cell) exchange one
             // 8-byte piece per head so that each stores 8 contiguous channels in one
             // 16-byte store -- even grp the mb = 0 block's, odd grp the mb = 1 block's
-            // -- halving the store instructions of the tile.
-            const bool odd = grp & 1;
+            // -- halving the store instructions of the tile. v_permlane16_swap(a, b)
+            // swaps the odd 16-lane rows of a with the even rows of b; with a = the
+            // mb = 0 piece and b = the mb = 1 piece, an even-row lane l is left with
+            // (a[l], a[l + 16]) and an odd-row lane with (b[l - 16], b[l]), which is
+            // that lane's 16 bytes in channel order.
             const long long base = bbase + ((long long)(ty0 + cell / kTileX) * G + tx0 + cell % kTileX) * C +
                                    32 * chh + 16 * (grp & 1) + 8 * (grp >> 1);
 #pragma unroll
@@ -977,11 +980,9 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
                     }
                     pk[mb] = make_uint2(pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3]));
                 }
-                const uint2 send = odd ? pk[0] : pk[1];
-                const uint2 recv = make_uint2(__shfl_xor(send.x, 16), __shfl_xor(send.y, 16));
-                const uint4 v = odd ? make_uint4(recv.x, recv.y, pk[1].x, pk[1].y)
-                                    : make_uint4(pk[0].x, pk[0].y, recv.x, recv.y);
-                *reinterpret_cast<uint4*>(Yg + base + o * kD) = v;
+                const auto sx = __builtin_amdgcn_permlane16_swap(pk[0].x, pk[1].x, false, false);
+                const auto sy = __builtin_amdgcn_permlane16_swap(pk[0].y, pk[1].y, false, false);
+                *reinterpret_cast<uint4*>(Yg + base + o * kD) = make_uint4(sx[0], sy[0], sx[1], sy[1]);
             }
         } else {
             const long long base =
