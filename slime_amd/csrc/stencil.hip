@@ -26,6 +26,7 @@
 #include "common.hpp"
 #include "kernels.hpp"
 #include "stencil_band.hpp"
+#include "stencil_sched.hpp"
 
 #include <cstring>
 #include <type_traits>
@@ -604,30 +605,18 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
     const int tpb = (G / kTileY) * tiles_x;
     const int ntiles = a.B * tpb;
 
-    // ---- this workgroup's tiles ------------------------------------------------------
-    // Workgroup i runs on XCD i % 8 (the dispatcher deals workgroups to the XCDs in
-    // turn), and XCD x takes the x-th eighth of the tiles. Each workgroup's first tile
-    // is fixed (the first nwx of the eighth); later ones are handed out in order by
-    // the XCD's ticket counter a.sched[x]. The tiles in flight on an XCD then stay a
-    // window of consecutive tiles, whose shared halo lines its L2 serves once: with a
-    // fixed stride the workgroups drift apart over a launch and neighbours fetch the
-    // same lines from HBM again (16 % more read traffic, 3 % more time at c3).
-    // a.sched[8 + x] counts the XCD's workgroups that have finished; the last one
-    // zeroes both counters for the next launch, which stream order puts after it.
-    const bool ticketed = (gridDim.x & 7) == 0 && (ntiles & 7) == 0;
-    const int xcd = blockIdx.x & 7, span = ntiles >> 3, nwx = gridDim.x >> 3;
-    const int first = nwx < span ? nwx : span;  // tiles of an eighth handed out fixed
-    int t_cur, t_stride, t_end;
-    if (ticketed) {
-        t_cur = xcd * span + (blockIdx.x >> 3);
-        t_stride = 0;
-        t_end = xcd * span + span;
-    } else {
-        t_cur = blockIdx.x;
-        t_stride = gridDim.x;
-        t_end = ntiles;
-    }
-    if (t_cur >= t_end) return;  // ticketed: blockIdx.x / 8 >= first, not counted in sched[8 + x]
+    // ---- this workgroup's tiles (stencil_sched.hpp) -----------------------------------
+    // Ticketed: the XCD's counter a.sched[x] hands out its eighth of the tiles in order
+    // after the fixed first ones, so the tiles in flight on an XCD stay a window of
+    // consecutive tiles, whose shared halo lines its L2 serves once: with a fixed
+    // stride the workgroups drift apart over a launch and neighbours fetch the same
+    // lines from HBM again (16 % more read traffic, 3 % more time at c3).
+    // a.sched[8 + x] counts the XCD's finished workgroups; the last one zeroes both
+    // counters for the next launch, which stream order puts after it.
+    const sched::StencilWalk walk = sched::stencil_walk(blockIdx.x, gridDim.x, ntiles);
+    const bool ticketed = walk.ticketed;
+    int t_cur = walk.t_cur;
+    if (!sched::has_tile(walk)) return;  // not one of the XCD's counted workgroups
     __shared__ int sTicket;
 
     const int cb = wave >> 1, chh = wave & 1;   // cell block, channel half
@@ -800,8 +789,8 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
         // through LDS before the last head, which starts that tile's loads.
         int ticket = 0;
         if (ticketed && tid == 0)
-            ticket = (int)__hip_atomic_fetch_add(a.sched + xcd, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        int t_next = !ticketed && t_cur + t_stride < t_end ? t_cur + t_stride : -1;
+            ticket = (int)__hip_atomic_fetch_add(a.sched + walk.xcd, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        int t_next = ticketed ? -1 : sched::strided_next(walk, t_cur);
         const int b = t_cur / tpb, tile = t_cur % tpb;
         const int ty0 = (tile / tiles_x) * kTileY, tx0 = (tile % tiles_x) * kTileX;
         const long long bbase = (long long)b * G * G * C;
@@ -825,8 +814,7 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
             // write follows the tile-end barrier.
             if (ticketed && h == 1 && tid == 0) sTicket = ticket;
             if (ticketed && h == H - 1) {
-                const int tk = __builtin_amdgcn_readfirstlane(sTicket);
-                t_next = first + tk < span ? xcd * span + first + tk : -1;
+                t_next = sched::ticket_tile(walk, __builtin_amdgcn_readfirstlane(sTicket));
             }
             if (h + 1 < H) {
                 issue_head(h + 1, nxt);
@@ -1029,13 +1017,13 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
         if (t_next < 0) break;
         t_cur = t_next;
     }
-    // Every grab of this workgroup has returned (the last one ended the loop), so the
-    // last of the XCD's `first` workgroups to count itself here resets the counters.
+    // Every draw of this workgroup has returned (the last one ended the loop), so the
+    // last of the XCD's counted workgroups to count itself here resets the counters.
     if (ticketed && tid == 0 &&
-        __hip_atomic_fetch_add(a.sched + 8 + xcd, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-            (unsigned)first - 1u) {
-        __hip_atomic_store(a.sched + xcd, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(a.sched + 8 + xcd, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        sched::last_finisher(walk, __hip_atomic_fetch_add(a.sched + 8 + walk.xcd, 1u, __ATOMIC_RELAXED,
+                                                          __HIP_MEMORY_SCOPE_AGENT))) {
+        __hip_atomic_store(a.sched + walk.xcd, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(a.sched + 8 + walk.xcd, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
