@@ -14,8 +14,9 @@
 // wave issues the 32 MFMAs of slab k from one buffer, it reads slab k+1's
 // fragments into the other and issues the loads of slab k+4, so the matrix cores
 // never wait for an LDS round trip; one barrier per slab publishes slab k+1 and
-// frees the stage of slab k. Stages are laid out in fragment order (each MFMA
-// operand read is one linear 1 KiB block: no bank conflicts). The first MFMA of
+// frees the stage of slab k. Each tile row's 64 slab bytes sit as four 16-byte
+// chunks XOR-swizzled by the row (gemm_addr.hpp), which keeps the operand reads
+// free of LDS bank conflicts. The first MFMA of
 // a tile starts from a zero accumulator instead of clearing 256 registers. The
 // weights are the MFMA "A" operand: a lane's accumulators hold 4 consecutive
 // output channels of one cell. The bf16 epilogue goes through LDS so that stores

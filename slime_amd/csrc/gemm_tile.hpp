@@ -17,10 +17,10 @@ namespace {
 // Tile shape, ring and staging constants, and all address arithmetic: gemm_addr.hpp.
 // Stage layout: tile row r (0..255 cells, 256..511 output channels) holds its 64
 // slab bytes at r*64, as four 16-byte chunks XOR-permuted by
-// f(r) = ((r >> 1) ^ (r >> 3)) & 3: physical chunk = logical chunk ^ f(r). One
+// f(r) = row_swz(r) = (r >> 2) & 3: physical chunk = logical chunk ^ f(r). One
 // direct-load instruction fills 16 whole rows (1 KiB, four lanes per 64-byte row),
 // and the operand reads -- 32 consecutive rows at one logical chunk per half
-// wave -- spread over the LDS banks.
+// wave -- fall in distinct LDS bank groups in every pass (gemm_addr.hpp).
 using namespace gemm_addr;
 
 __device__ __forceinline__ float apply_act(float v, int act) {

@@ -505,8 +505,9 @@ __global__ __launch_bounds__((Layout<T, D>::kThreads), 2) void stencil_kernel(St
 // head, so the only barrier per head is the one that publishes the staged halo.
 // Growth, update and head mixing then run in registers for its 16 x 32 outputs.
 //
-// The kernel is persistent: a workgroup walks a run of tiles (XCD-contiguous), and
-// the staging pipeline runs across tile boundaries -- head 0 of the next tile and
+// The kernel is persistent: a workgroup takes tiles of its XCD's eighth in order from
+// the XCD's ticket counter (stencil_sched.hpp), and the staging pipeline runs across
+// tile boundaries -- head 0 of the next tile and
 // that tile's parameters are in flight while the last head of the current one
 // computes -- so no workgroup starts from an empty pipeline.
 namespace mf {
