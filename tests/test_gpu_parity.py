@@ -511,3 +511,35 @@ def test_c3_shape_conserves_mass_and_matches_oracle_on_one_batch(oracle):
     print(f"  batch 0 of c3: normalised error {err:.3e}")
     assert err <= TOL["bf16"]
     np.testing.assert_allclose(mi[0], rmi[0], rtol=1e-6)
+
+
+def test_c3_bench_call_conserves_mass_and_repeats_bitwise():
+    # The benched call: 10 chained c3 steps in one slime_ca_step (each step's mass
+    # scale folded into the next step's weights and loads, the last step written in
+    # fp32 and rescaled once), run twice on one handle. At this size the checks are
+    # size-independent: every value finite, the stored state's per-(batch, head) sums
+    # equal the input's up to one bf16 rounding of each element, and the second call
+    # repeats the first bit for bit (the stencil's tile tickets decide which
+    # workgroup runs a tile, never what it computes). One step of batch 0 is
+    # compared with the oracle by the test above.
+    from slime_amd import CONFIGS
+    cfg = CONFIGS["c3"]
+    p, X = _prep(cfg)
+
+    def head_sums(t):
+        return t.to(torch.float64).reshape(cfg.B, -1, cfg.H, cfg.D).sum(dim=(1, 3)).cpu().numpy()
+
+    with _engine(cfg) as e:
+        e.set_params(p)
+        x = _dev(X, "bf16")
+        y1 = e.forward(x, n_steps=10)
+        y2 = e.forward(x, n_steps=10)
+        torch.cuda.synchronize()
+        mi, mo = e.mass()
+        assert bool(torch.isfinite(y1.float()).all())
+        assert torch.equal(y1, y2)
+        s_in, s_out = head_sums(x), head_sums(y1)
+    np.testing.assert_allclose(mo, mi, rtol=1e-6)
+    drift = np.abs(s_out - s_in) / np.abs(s_in)
+    print(f"  10 chained c3 steps: max relative drift of the stored head sums {drift.max():.2e}")
+    assert drift.max() <= 5e-5
