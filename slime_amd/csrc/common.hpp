@@ -117,12 +117,29 @@ __device__ __forceinline__ float rcp_fast(float x) { return __builtin_amdgcn_rcp
 
 // tanh-GELU written as x * sigmoid(2u), u = sqrt(2/pi) (x + 0.044715 x^3):
 // 0.5 x (1 + tanh u) = x / (1 + exp(-2u)). exp(-2u) = 2^(x (k0 + k1 x^2)).
+constexpr float kGeluK0 = -2.0f * 0.7978845608028654f * 1.4426950408889634f;
+constexpr float kGeluK1 = kGeluK0 * 0.044715f;
 __device__ __forceinline__ float gelu_tanh(float x) {
-    constexpr float kLog2e = 1.4426950408889634f;
-    constexpr float k0 = -2.0f * 0.7978845608028654f * kLog2e;
-    constexpr float k1 = k0 * 0.044715f;
-    const float e = exp2_fast(x * __builtin_fmaf(k1, x * x, k0));
+    const float e = exp2_fast(x * __builtin_fmaf(kGeluK1, x * x, kGeluK0));
     return x * rcp_fast(1.0f + e);
+}
+
+// gelu_tanh of N independent values in place, one stage at a time over all of them,
+// so that their transcendentals issue back to back. Per value the operations and
+// their order are those of gelu_tanh, and so are the results.
+template <int N>
+__device__ __forceinline__ void gelu_tanh_n(float (&v)[N]) {
+    float t[N];
+#pragma unroll
+    for (int e = 0; e < N; ++e) t[e] = v[e] * v[e];
+#pragma unroll
+    for (int e = 0; e < N; ++e) t[e] = __builtin_fmaf(kGeluK1, t[e], kGeluK0);
+#pragma unroll
+    for (int e = 0; e < N; ++e) t[e] = exp2_fast(v[e] * t[e]);
+#pragma unroll
+    for (int e = 0; e < N; ++e) t[e] = rcp_fast(1.0f + t[e]);
+#pragma unroll
+    for (int e = 0; e < N; ++e) v[e] = v[e] * t[e];
 }
 
 }  // namespace slime

@@ -300,14 +300,27 @@ __device__ __forceinline__ void convert_tile(f32x16 (&acc)[4][4], OutBuf& ob) {
             pin_acc(acc[2 * p][j]);
             pin_acc(acc[2 * p + 1][j]);
 #pragma unroll
-            for (int ii = 0; ii < 2; ++ii)
+            for (int ii = 0; ii < 2; ++ii) {
+                const int i = 2 * p + ii;
+                if constexpr (kAct == 2) {
+                    // GELU of the block's 16 values stage by stage: their exp2 and rcp
+                    // issue back to back instead of one value's chain at a time.
+                    float v[16];
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int i = 2 * p + ii;
-                    ob.v[2 * j + p][4 * ii + q] = make_uint2(
-                        pack_bf16x2(act_of<kAct>(acc[i][j][4 * q + 0]), act_of<kAct>(acc[i][j][4 * q + 1])),
-                        pack_bf16x2(act_of<kAct>(acc[i][j][4 * q + 2]), act_of<kAct>(acc[i][j][4 * q + 3])));
+                    for (int e = 0; e < 16; ++e) v[e] = acc[i][j][e];
+                    gelu_tanh_n(v);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        ob.v[2 * j + p][4 * ii + q] = make_uint2(pack_bf16x2(v[4 * q + 0], v[4 * q + 1]),
+                                                                 pack_bf16x2(v[4 * q + 2], v[4 * q + 3]));
+                } else {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        ob.v[2 * j + p][4 * ii + q] = make_uint2(
+                            pack_bf16x2(act_of<kAct>(acc[i][j][4 * q + 0]), act_of<kAct>(acc[i][j][4 * q + 1])),
+                            pack_bf16x2(act_of<kAct>(acc[i][j][4 * q + 2]), act_of<kAct>(acc[i][j][4 * q + 3])));
                 }
+            }
         }
 }
 
