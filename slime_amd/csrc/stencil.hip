@@ -522,14 +522,16 @@ constexpr int kBufB = (3 * kHaloPad + kTileCells) * kRowB;  // 28 KiB
 constexpr int kWC = 16;                                     // cells per wave
 constexpr int kAttB = kWC * kRowB;                          // one 16 x 64 bf16 matrix
 constexpr int kS9 = 12;  // floats per cell in a score buffer (9 used, 9..11 take discards)
-// Per-tile parameter block (fp32): M[8][8] (M[o][h] at o*8+h), mu[8], sigma[8],
-// scale[8] and its low part[8]; then, for per-cell growth, mu and sigma [cell][8];
-// then the pod's 3x3-kernel band table (stencil_band.hpp), 12 dwords per head.
-constexpr int kPM = 0, kPMu = 64, kPSg = 72, kPSc = 80, kPScLo = 88, kPScal = 96;
+// Per-tile parameter block (fp32): M transposed (M[o][h] at h*8+o, so that head h's
+// eight mixing weights are two 16-byte reads); per head h at kPH + 4h the deferred
+// mass scale of X, its low part, mu and sigma (one 16-byte read); then, for per-cell
+// growth, mu and sigma [cell][8]; then the pod's 3x3-kernel band table
+// (stencil_band.hpp), 12 dwords per head.
+constexpr int kPM = 0, kPH = 64, kPScal = 96;
 constexpr int kPCellMu = 96, kPCellSg = 96 + kTileCells * 8, kPBand = 96 + 2 * kTileCells * 8;
 constexpr int kBandHead = 12;                       // dwords per head: 3 runs x {A, B} x {hi, lo}
 constexpr int kParF = kPBand + kHeads * kBandHead;
-static_assert(kPBand % 4 == 0, "band table rows are read as 16-byte vectors");
+static_assert(kPBand % 4 == 0 && kPH % 4 == 0, "16-byte reads of the band table and the per-head values");
 
 // 16-byte chunk swizzles inside a 128-byte row. X and V: any four consecutive
 // rows 4j..4j+3, and rows {r, r+2, r+8, r+10}, occupy disjoint chunk pairs, so
@@ -674,13 +676,14 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
         const int pod = b / a.per_pod;
         pre[0] = pre[1] = pre[2] = 0.f;
         if (tid < H * kBandHead) pre_band = kband[pod * H * kBandHead + tid];
-        if (tid < kPM + 64) pre[0] = a.M[pod * 64 + tid - kPM];
-        else if (tid < kPSg + 8) {
-            if (!a.per_cell) pre[0] = tid < kPSg ? a.mu[pod * 8 + tid - kPMu] : a.sigma[pod * 8 + tid - kPSg];
-        } else if (tid < kPScLo) {
-            pre[0] = a.scale_in ? a.scale_in[b * 8 + tid - kPSc] : 1.0f;
+        if (tid < kPM + 64) {
+            const int hh = (tid - kPM) >> 3, o = (tid - kPM) & 7;
+            pre[0] = a.M[pod * 64 + o * 8 + hh];
         } else if (tid < kPScal) {
-            pre[0] = a.scale_in ? a.scale_in[a.B * 8 + b * 8 + tid - kPScLo] : 0.0f;
+            const int hh = (tid - kPH) >> 2, f = (tid - kPH) & 3;
+            if (f == 0) pre[0] = a.scale_in ? a.scale_in[b * 8 + hh] : 1.0f;
+            else if (f == 1) pre[0] = a.scale_in ? a.scale_in[a.B * 8 + b * 8 + hh] : 0.0f;
+            else if (!a.per_cell) pre[0] = f == 2 ? a.mu[pod * 8 + hh] : a.sigma[pod * 8 + hh];
         }
         if (a.per_cell) {
             const int ty0 = (tile / tiles_x) * kTileY, tx0 = (tile % tiles_x) * kTileX;
@@ -827,13 +830,21 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
 
             // ---- S4 scores of this wave's cells, kept for the 9 neighbours --------------
             {
+                // All operand reads first, then the MFMAs: the compiler would otherwise
+                // reuse registers and wait for each read in turn.
                 const uint4 pa0 = *reinterpret_cast<const uint4*>(buf + sp_off[0]);
                 const uint4 pa1 = *reinterpret_cast<const uint4*>(buf + sp_off[1]);
+                uint4 ib[3][2];
+#pragma unroll
+                for (int jj = 0; jj < 3; ++jj)
+#pragma unroll
+                    for (int ks = 0; ks < 2; ++ks) ib[jj][ks] = *reinterpret_cast<const uint4*>(buf + si_off[jj][ks]);
+                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int jj = 0; jj < 3; ++jj) {
                     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-                    acc = mfma16(pa0, *reinterpret_cast<const uint4*>(buf + si_off[jj][0]), acc);
-                    acc = mfma16(pa1, *reinterpret_cast<const uint4*>(buf + si_off[jj][1]), acc);
+                    acc = mfma16(pa0, ib[jj][0], acc);
+                    acc = mfma16(pa1, ib[jj][1], acc);
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
                         *reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(s9) + s9_off[jj][e]) =
@@ -888,34 +899,45 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
                                                __builtin_amdgcn_perm(t.w, t.z, band_sel[ks][3]));
                     }
                 }
-                f32x4 u[2], vt[2];
+                // The 16 transposing reads of X and V first, then the 16 MFMAs.
+                uint4 ax[2][2], av[2][2];  // [mb][ks]
 #pragma unroll
-                for (int mb = 0; mb < 2; ++mb) {
-                    u[mb] = vt[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+                for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
                     for (int ks = 0; ks < 2; ++ks) {
                         const uint2 x0 = read_tr16(buf + offX + tr_off[mb][ks][0]);
                         const uint2 x1 = read_tr16(buf + offX + tr_off[mb][ks][1]);
                         const uint2 v0 = read_tr16(buf + offV + tr_off[mb][ks][0]);
                         const uint2 v1 = read_tr16(buf + offV + tr_off[mb][ks][1]);
-                        const uint4 ax = make_uint4(x0.x, x0.y, x1.x, x1.y);
-                        const uint4 av = make_uint4(v0.x, v0.y, v1.x, v1.y);
+                        ax[mb][ks] = make_uint4(x0.x, x0.y, x1.x, x1.y);
+                        av[mb][ks] = make_uint4(v0.x, v0.y, v1.x, v1.y);
+                    }
+                __builtin_amdgcn_sched_barrier(0);
+                f32x4 u[2], vt[2];
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb) {
+                    u[mb] = vt[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
                         for (int m = 0; m < 2; ++m) {
-                            u[mb] = mfma16(ax, kq[ks][m], u[mb]);
-                            vt[mb] = mfma16(av, aw[ks][m], vt[mb]);
+                            u[mb] = mfma16(ax[mb][ks], kq[ks][m], u[mb]);
+                            vt[mb] = mfma16(av[mb][ks], aw[ks][m], vt[mb]);
                         }
-                    }
                 }
-                const float s_in = par[kPSc + h];  // deferred mass scale of X (high part)
-                const float s_lo = par[kPScLo + h];
+                const float4 ph = *reinterpret_cast<const float4*>(par + kPH + 4 * h);
+                const float s_in = ph.x, s_lo = ph.y;  // deferred mass scale of X, high and low parts
                 const float two_dt = 2.0f * dt;
                 float mw[H];
-#pragma unroll
-                for (int o = 0; o < H; ++o) mw[o] = par[kPM + o * H + h];
+                {
+                    const float4 m0 = *reinterpret_cast<const float4*>(par + kPM + h * H);
+                    const float4 m1 = *reinterpret_cast<const float4*>(par + kPM + h * H + 4);
+                    mw[0] = m0.x, mw[1] = m0.y, mw[2] = m0.z, mw[3] = m0.w;
+                    mw[4] = m1.x, mw[5] = m1.y, mw[6] = m1.z, mw[7] = m1.w;
+                }
                 // (U s - mu) / (sigma + 1e-7) * sqrt(log2 e) = U ga - gb
-                const float mu_h = a.per_cell ? par[kPCellMu + cell * 8 + h] : par[kPMu + h];
-                const float sg_h = a.per_cell ? par[kPCellSg + cell * 8 + h] : par[kPSg + h];
+                const float mu_h = a.per_cell ? par[kPCellMu + cell * 8 + h] : ph.z;
+                const float sg_h = a.per_cell ? par[kPCellSg + cell * 8 + h] : ph.w;
                 const float gsc = sqrt_log2e / (sg_h + 1e-7f);
                 const float ga = gsc * s_in, gb = mu_h * gsc;
                 float xacc = 0.f;
