@@ -851,6 +851,47 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
                             acc[e];
                 }
             }
+            // ---- S2: U = X_halo^T . Kmat^T on the matrix cores. It does not depend on the
+            // softmax, so its operand reads and MFMAs go first and overlap that chain.
+            uint4 kq[2][2];  // Kmat^T [ks][hi/lo], from the head's band-table run
+            {
+                const unsigned* kb = reinterpret_cast<const unsigned*>(par) + kPBand + h * kBandHead;
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks) {
+                    const uint4 t = *reinterpret_cast<const uint4*>(kb + band_row[ks]);  // A, B hi; A, B lo
+                    kq[ks][0] = make_uint4(__builtin_amdgcn_perm(t.y, t.x, band_sel[ks][0]),
+                                           __builtin_amdgcn_perm(t.y, t.x, band_sel[ks][1]),
+                                           __builtin_amdgcn_perm(t.y, t.x, band_sel[ks][2]),
+                                           __builtin_amdgcn_perm(t.y, t.x, band_sel[ks][3]));
+                    kq[ks][1] = make_uint4(__builtin_amdgcn_perm(t.w, t.z, band_sel[ks][0]),
+                                           __builtin_amdgcn_perm(t.w, t.z, band_sel[ks][1]),
+                                           __builtin_amdgcn_perm(t.w, t.z, band_sel[ks][2]),
+                                           __builtin_amdgcn_perm(t.w, t.z, band_sel[ks][3]));
+                }
+            }
+            // The 16 transposing reads of X and V first (both are needed below).
+            uint4 ax[2][2], av[2][2];  // [mb][ks]
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks) {
+                    const uint2 x0 = read_tr16(buf + offX + tr_off[mb][ks][0]);
+                    const uint2 x1 = read_tr16(buf + offX + tr_off[mb][ks][1]);
+                    const uint2 v0 = read_tr16(buf + offV + tr_off[mb][ks][0]);
+                    const uint2 v1 = read_tr16(buf + offV + tr_off[mb][ks][1]);
+                    ax[mb][ks] = make_uint4(x0.x, x0.y, x1.x, x1.y);
+                    av[mb][ks] = make_uint4(v0.x, v0.y, v1.x, v1.y);
+                }
+            __builtin_amdgcn_sched_barrier(0);
+            f32x4 u[2];
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb) {
+                u[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                    for (int m = 0; m < 2; ++m) u[mb] = mfma16(ax[mb][ks], kq[ks][m], u[mb]);
+            }
             // ---- softmax; Att of this wave's cells (its own LDS: in order, no barrier) -
             {
                 const float* srow = s9 + sc * kS9;
@@ -875,56 +916,10 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
                 }
             }
 
-            // ---- S2 / S5 on the matrix cores, then S3, S6 and head mixing -----------------
+            // ---- S3 from U, then S5 on the matrix cores, S6 and head mixing --------------
             {
-                uint4 aw[2][2];  // Att^T [ks][hi/lo]
-#pragma unroll
-                for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-                    for (int m = 0; m < 2; ++m)
-                        aw[ks][m] = *reinterpret_cast<const uint4*>(att + m * kAttB + at_off[ks]);
-                uint4 kq[2][2];  // Kmat^T [ks][hi/lo], from the head's band-table run
-                {
-                    const unsigned* kb = reinterpret_cast<const unsigned*>(par) + kPBand + h * kBandHead;
-#pragma unroll
-                    for (int ks = 0; ks < 2; ++ks) {
-                        const uint4 t = *reinterpret_cast<const uint4*>(kb + band_row[ks]);  // A, B hi; A, B lo
-                        kq[ks][0] = make_uint4(__builtin_amdgcn_perm(t.y, t.x, band_sel[ks][0]),
-                                               __builtin_amdgcn_perm(t.y, t.x, band_sel[ks][1]),
-                                               __builtin_amdgcn_perm(t.y, t.x, band_sel[ks][2]),
-                                               __builtin_amdgcn_perm(t.y, t.x, band_sel[ks][3]));
-                        kq[ks][1] = make_uint4(__builtin_amdgcn_perm(t.w, t.z, band_sel[ks][0]),
-                                               __builtin_amdgcn_perm(t.w, t.z, band_sel[ks][1]),
-                                               __builtin_amdgcn_perm(t.w, t.z, band_sel[ks][2]),
-                                               __builtin_amdgcn_perm(t.w, t.z, band_sel[ks][3]));
-                    }
-                }
-                // The 16 transposing reads of X and V first, then the 16 MFMAs.
-                uint4 ax[2][2], av[2][2];  // [mb][ks]
-#pragma unroll
-                for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-                    for (int ks = 0; ks < 2; ++ks) {
-                        const uint2 x0 = read_tr16(buf + offX + tr_off[mb][ks][0]);
-                        const uint2 x1 = read_tr16(buf + offX + tr_off[mb][ks][1]);
-                        const uint2 v0 = read_tr16(buf + offV + tr_off[mb][ks][0]);
-                        const uint2 v1 = read_tr16(buf + offV + tr_off[mb][ks][1]);
-                        ax[mb][ks] = make_uint4(x0.x, x0.y, x1.x, x1.y);
-                        av[mb][ks] = make_uint4(v0.x, v0.y, v1.x, v1.y);
-                    }
-                __builtin_amdgcn_sched_barrier(0);
-                f32x4 u[2], vt[2];
-#pragma unroll
-                for (int mb = 0; mb < 2; ++mb) {
-                    u[mb] = vt[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                    for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-                        for (int m = 0; m < 2; ++m) {
-                            u[mb] = mfma16(ax[mb][ks], kq[ks][m], u[mb]);
-                            vt[mb] = mfma16(av[mb][ks], aw[ks][m], vt[mb]);
-                        }
-                }
+                // S3 and the scaled X need only U and the parameters: they run while the
+                // Att values land and the S5 MFMAs work; exp2 over all 8 values at once.
                 const float4 ph = *reinterpret_cast<const float4*>(par + kPH + 4 * h);
                 const float s_in = ph.x, s_lo = ph.y;  // deferred mass scale of X, high and low parts
                 const float two_dt = 2.0f * dt;
@@ -940,6 +935,18 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
                 const float sg_h = a.per_cell ? par[kPCellSg + cell * 8 + h] : ph.w;
                 const float gsc = sqrt_log2e / (sg_h + 1e-7f);
                 const float ga = gsc * s_in, gb = mu_h * gsc;
+                float coef[2][4], xcs[2][4], ex[2][4];  // dt * g, scaled X, bell argument
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float tg = __builtin_fmaf(u[mb][e], ga, -gb);
+                        ex[mb][e] = -tg * tg;
+                    }
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) ex[mb][e] = exp2_fast(ex[mb][e]);
                 float xacc = 0.f;
 #pragma unroll
                 for (int mb = 0; mb < 2; ++mb) {
@@ -947,16 +954,34 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
                     const float xv[4] = {bf16lo(xr.x), bf16hi(xr.x), bf16lo(xr.y), bf16hi(xr.y)};
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        const float tg = __builtin_fmaf(u[mb][e], ga, -gb);
-                        const float ex = exp2_fast(-tg * tg);
-                        const float coef = __builtin_fmaf(ex, two_dt, -dt);  // dt * g
-                        const float xc = __builtin_fmaf(xv[e], s_lo, xv[e] * s_in);
-                        const float z = __builtin_fmaf(coef, vt[mb][e], xc);
-                        xacc += xc;
+                        coef[mb][e] = __builtin_fmaf(ex[mb][e], two_dt, -dt);
+                        xcs[mb][e] = __builtin_fmaf(xv[e], s_lo, xv[e] * s_in);
+                        xacc += xcs[mb][e];
+                    }
+                }
+                uint4 aw[2][2];  // Att^T [ks][hi/lo]
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                    for (int m = 0; m < 2; ++m)
+                        aw[ks][m] = *reinterpret_cast<const uint4*>(att + m * kAttB + at_off[ks]);
+                f32x4 vt[2];
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb) {
+                    vt[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                        for (int m = 0; m < 2; ++m) vt[mb] = mfma16(av[mb][ks], aw[ks][m], vt[mb]);
+                }
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float z = __builtin_fmaf(coef[mb][e], vt[mb][e], xcs[mb][e]);
 #pragma unroll
                         for (int o = 0; o < H; ++o) y[o][mb][e] = __builtin_fmaf(mw[o], z, y[o][mb][e]);
                     }
-                }
 #pragma unroll
                 for (int j = 0; j < H; ++j) xin[j] = (j == h) ? xacc : xin[j];
             }
