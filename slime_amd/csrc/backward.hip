@@ -357,14 +357,25 @@ __global__ __launch_bounds__(256) void bw_cell_kernel(BackwardArgs a) {
             sa = __builtin_fmaf(s[k], ga[k], sa);
         }
         float gp[4] = {0.f, 0.f, 0.f, 0.f};
+        float tape_a = 0.f, tape_gs = 0.f;  // kL >= 9: lane li < 9 holds a_li and gs_li
 #pragma unroll
         for (int k = 0; k < 9; ++k) {
             const float gs = s[k] * (ga[k] - sa);
 #pragma unroll
             for (int e = 0; e < 4; ++e) gp[e] = __builtin_fmaf(gs * inv_sqrt_d, ik[k].v[e], gp[e]);
-            if (k % kL == li) {  // the tape for the gathers: a_k and gs_k per (r, h)
+            // the tape for the gathers: a_k and gs_k per (r, h)
+            if constexpr (kL >= 9) {
+                tape_a = k == li ? s[k] : tape_a;
+                tape_gs = k == li ? gs : tape_gs;
+            } else if (k % kL == li) {
                 a.att[(r * H + h) * 9 + k] = s[k];
                 a.gS[(r * H + h) * 9 + k] = gs;
+            }
+        }
+        if constexpr (kL >= 9) {  // one store of each per lane instead of one per k
+            if (li < 9) {
+                a.att[(r * H + h) * 9 + li] = tape_a;
+                a.gS[(r * H + h) * 9 + li] = tape_gs;
             }
         }
         st4f(a.gU, ir, gu);
