@@ -56,6 +56,15 @@ def load_traffic(kernel: str, workload: str):
         return None
 
 
+def load_ceilings() -> dict:
+    """Rates measured on the card (profiles/ceilings.json); empty when not committed."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "ceilings.json")) as f:
+            return {k: v for k, v in json.load(f).items() if not k.startswith("_")}
+    except (OSError, ValueError):
+        return {}
+
+
 def cpu_model() -> str:
     """The host CPU's model name (as lscpu reports it, from /proc/cpuinfo)."""
     try:
@@ -189,8 +198,17 @@ def main() -> int:
                             "peak": PEAK_TFLOPS[cfg.dtype], "unit": "TFLOP/s", "avg_ms": gemm_ms,
                             "algorithmic_flops": gf, "traffic": load_traffic("gemm", wl)},
     }
-    for k in kernels.values():
+    # Beside the datasheet fractions: the fraction of what the card sustains (the
+    # stencil reads four planes and writes one, a copy-like stream; the GEMM against a
+    # register-only MFMA loop).
+    ceil = load_ceilings()
+    measured = {"stencil": ceil.get("hbm_copy_gbs"),
+                "projection_gemm": ceil.get("mfma_bf16_tflops_random") if cfg.dtype == "bf16" else None}
+    for name, k in kernels.items():
         k["frac"] = k["achieved"] / k["peak"]
+        if measured[name]:
+            k["measured_peak"] = measured[name]
+            k["frac_of_measured"] = k["achieved"] / measured[name]
     dom_name = "stencil" if sten_ms >= gemm_ms else "projection_gemm"
     dom = kernels[dom_name]
     roofline = {"kernel": dom_name, "bound": dom["bound"], "achieved": dom["achieved"],
