@@ -237,6 +237,26 @@ def test_tile_tickets_cover_every_tile_on_each_launch(oracle):
             np.testing.assert_allclose(mo, mi, rtol=1e-6)
 
 
+def test_fixed_stride_tile_walk_when_the_tile_count_is_not_a_multiple_of_eight(oracle):
+    # 37 x (24 / 4) x (24 / 8) = 666 tiles: not a multiple of 8, so the stencil takes
+    # the fixed-stride walk instead of the per-XCD tickets, and with more tiles than
+    # the persistent grid some workgroups take a second tile. The 24 x 24 grid's
+    # 21,312 cells are not a multiple of 256, so the projections take the plain GEMM.
+    cfg = _cfg("stride", B=37, G=24, D=64, dtype="bf16")
+    p, X = _prep(cfg)
+    with _engine(cfg) as e:
+        e.set_params(p)
+        y = e.forward(_dev(X, "bf16"), n_steps=2)
+        torch.cuda.synchronize()
+        mi, mo = e.mass()
+        Y = _host(y)
+    ref, rmi, _ = oracle.step(_ocfg(cfg), X, p, 2)
+    errs = [norm_err(Y[b], ref[b]) for b in range(cfg.B)]
+    print(f"  2 steps: max normalised error over batches {max(errs):.3e}")
+    assert max(errs) <= TOL["bf16"], (int(np.argmax(errs)), max(errs))
+    np.testing.assert_allclose(mo, mi, rtol=1e-6)
+
+
 def test_multi_step_bf16_conserves_mass_and_tracks_oracle(oracle):
     # Two steps in one call: the second folds the first step's mass scale into its
     # weights and X loads; mass is conserved against the caller's input.
