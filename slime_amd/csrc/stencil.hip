@@ -709,6 +709,13 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
     set_tile(t_cur);
     fetch_params(t_cur);
     issue_head(0, bufA);
+    // Head 0's loads are always waited for before the head-0 barrier is reached (here
+    // for the first tile, at the previous tile's end otherwise), so that barrier does
+    // not wait for the previous tile's Y stores, the youngest memory operations then.
+    // The empty statement marks the parameter registers as produced after that wait,
+    // or the compiler adds a full wait for their loads at the head-0 barrier.
+    wait_vm0();
+    asm volatile("" : "+v"(pre[0]), "+v"(pre[1]), "+v"(pre[2]), "+v"(pre_band));
 
     // ---- per-lane roles (tile independent) ----------------------------------------------
     unsigned char* att = sAtt + wave * 2 * kAttB;
@@ -789,11 +796,10 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
     float xin[H];
     int gh = 0;  // heads processed by this workgroup (selects the staging buffer)
     while (true) {
-        // The next tile: fixed stride, or the ticket thread 0 draws now and publishes
-        // through LDS before the last head, which starts that tile's loads.
+        // The next tile: fixed stride, or the ticket thread 0 draws after head 1's
+        // barrier and publishes through LDS before the last head, which starts that
+        // tile's loads.
         int ticket = 0;
-        if (ticketed && tid == 0)
-            ticket = (int)__hip_atomic_fetch_add(a.sched + walk.xcd, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         int t_next = ticketed ? -1 : sched::strided_next(walk, t_cur);
         const int b = t_cur / tpb, tile = t_cur % tpb;
         const int ty0 = (tile / tiles_x) * kTileY, tx0 = (tile % tiles_x) * kTileX;
@@ -811,12 +817,21 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
         for (int h = 0; h < H; ++h, ++gh) {
             const unsigned char* buf = (gh & 1) ? bufB : bufA;
             unsigned char* nxt = (gh & 1) ? bufA : bufB;
-            wait_vm0();       // this wave's loads of head h have landed
-            __syncthreads();  // ... and every other wave's; head h-1 is fully consumed
+            if (h > 0) wait_vm0();  // this wave's loads of head h have landed
+            __syncthreads();        // ... and every other wave's; head h-1 is fully consumed
             if (h == 0) store_params(par);
-            // Written after head 1's barrier, read after head H-1's; the next tile's
-            // write follows the tile-end barrier.
-            if (ticketed && h == 1 && tid == 0) sTicket = ticket;
+            // Drawn after head 1's barrier, when nothing else is in flight; written after
+            // head 2's, whose wait has covered the draw, and read after head H-1's. The
+            // next tile's write follows the tile-end barrier.
+            if (ticketed && h == 1 && tid == 0) {
+                // An address the compiler cannot prove uniform keeps the draw a plain
+                // per-lane atomic, whose result is waited for at its use; as a uniform
+                // one it is rewritten into a wave-wide form that waits at once.
+                auto* ctr = (__attribute__((address_space(1))) unsigned*)(a.sched + walk.xcd);
+                asm volatile("" : "+v"(ctr));
+                ticket = (int)__hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            if (ticketed && h == 2 && tid == 0) sTicket = ticket;
             if (ticketed && h == H - 1) {
                 t_next = sched::ticket_tile(walk, __builtin_amdgcn_readfirstlane(sTicket));
             }
@@ -988,6 +1003,9 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
         }
 
         // ---- store Y and the tile's mass partial sums -----------------------------------
+        // The next tile's parameters and head-0 loads have had the last head to land.
+        wait_vm0();
+        asm volatile("" : "+v"(pre[0]), "+v"(pre[1]), "+v"(pre[2]), "+v"(pre_band));
         TY* Yg = static_cast<TY*>(a.Y);
         float ysum[H];  // this lane's sum of stored Y per head
 #pragma unroll
