@@ -60,6 +60,32 @@ __device__ __forceinline__ F4 ld4(const void* p, long long i) {  // i: a multipl
     }
     return r;
 }
+// Four channels as loaded, converted at each use: two packed bf16 pairs or four floats.
+template <typename T>
+using Raw4 = std::conditional_t<sizeof(T) == 2, uint2, float4>;
+template <typename T>
+__device__ __forceinline__ Raw4<T> ldraw4(const void* p, long long i) {
+    return *reinterpret_cast<const Raw4<T>*>(static_cast<const T*>(p) + i);
+}
+template <typename T>
+__device__ __forceinline__ float raw_at(const Raw4<T>& r, int e) {
+    if constexpr (sizeof(T) == 2) {
+        const unsigned w = e < 2 ? r.x : r.y;
+        return (e & 1) ? bf16hi(w) : bf16lo(w);
+    } else {
+        return e == 0 ? r.x : e == 1 ? r.y : e == 2 ? r.z : r.w;
+    }
+}
+// Marks the loaded values as rewritten here, so the compiler converts them again at
+// the next use instead of keeping the converted floats live in between.
+template <typename T>
+__device__ __forceinline__ void reuse_raw(Raw4<T> (&r)[9]) {
+#pragma unroll
+    for (int k = 0; k < 9; ++k) {
+        if constexpr (sizeof(T) == 2) asm volatile("" : "+v"(r[k].x), "+v"(r[k].y));
+        else asm volatile("" : "+v"(r[k].x), "+v"(r[k].y), "+v"(r[k].z), "+v"(r[k].w));
+    }
+}
 __device__ __forceinline__ F4 ld4f(const float* p, long long i) {
     const float4 f = *reinterpret_cast<const float4*>(p + i);
     return F4{{f.x, f.y, f.z, f.w}};
@@ -194,8 +220,11 @@ __device__ __forceinline__ float lanes_sum(float v) {
     return v;
 }
 
+// bf16: four waves per SIMD (128 VGPRs; a few bytes of spill), with the loaded
+// neighbours kept packed, K and M in LDS and the parameter partials in LDS.
 template <typename T, int kD>
-__global__ __launch_bounds__(256) void bw_cell_kernel(BackwardArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(sizeof(T) == 2 ? 4 : 2)))
+void bw_cell_kernel(BackwardArgs a) {
     constexpr int H = kHeads, C = H * kD, kL = kD / 4, kGroups = 256 / kL, kCpi = kGroups / H;
     static_assert(kL >= 2 && kL <= 16, "4 channels per lane, groups inside a DPP row");
     __shared__ __attribute__((aligned(16))) float sgy[kCpi * C];  // gY of the block's cells
@@ -220,17 +249,22 @@ __global__ __launch_bounds__(256) void bw_cell_kernel(BackwardArgs a) {
     const long long band = banded ? pod_cells / 8 : pod_cells;
     const float inv_sqrt_d = 1.0f / __builtin_sqrtf((float)kD);
     const float dt = a.dt;
-    float mcol[H];
+    // The pod's 3x3 weights K[h][k] and mixing columns M[o][h], read from LDS at each
+    // use (registers are what limits the waves per SIMD here).
+    __shared__ float skw[H * 9], smc[H * H];
+    if (threadIdx.x < H * 9) skw[threadIdx.x] = a.K[pod * H * 9 + threadIdx.x];
+    else if (threadIdx.x < H * 9 + H * H) {
+        const int j = threadIdx.x - H * 9, hh = j / H, o = j % H;  // smc[hh * H + o] = M[o][hh]
+        smc[j] = a.M[(pod * H + o) * H + hh];
+    }
+    __syncthreads();
+    const float* kw = skw + h * 9;
+    const float* mcol = smc + h * H;
+    // Each thread's parameter partials, accumulated in its own LDS column:
+    // gM[o][h] (8), gK[h][k] (9), gmu, gsigma.
+    __shared__ float red[kPartF][256];
 #pragma unroll
-    for (int o = 0; o < H; ++o) mcol[o] = a.M[(pod * H + o) * H + h];
-    float kw[9];
-#pragma unroll
-    for (int k = 0; k < 9; ++k) kw[k] = a.K[(pod * H + h) * 9 + k];
-    float pM[H], pK[9], pmu = 0.f, psg = 0.f;
-#pragma unroll
-    for (int o = 0; o < H; ++o) pM[o] = 0.f;
-#pragma unroll
-    for (int k = 0; k < 9; ++k) pK[k] = 0.f;
+    for (int q = 0; q < kPartF; ++q) red[q][threadIdx.x] = 0.f;
 
     for (long long i0 = (long long)wx * kCpi; i0 < band; i0 += (long long)nWx * kCpi) {
         const long long i = xcd * band + i0 + cs;
@@ -245,12 +279,12 @@ __global__ __launch_bounds__(256) void bw_cell_kernel(BackwardArgs a) {
             nb[k] = ((long long)b * cells + (long long)wrapb(y + k / 3 - 1, G) * G + wrapb(x + k % 3 - 1, G)) * C +
                     h * kD + c0;
         // ---- forward locals of head h at r (4 channels) ----
-        F4 xk[9], ik[9], vk[9];
+        Raw4<T> xk[9], ik[9], vk[9];
 #pragma unroll
         for (int k = 0; k < 9; ++k) {
-            xk[k] = ld4<T>(a.X, nb[k]);
-            ik[k] = ld4<T>(a.I, nb[k]);
-            vk[k] = ld4<T>(a.V, nb[k]);
+            xk[k] = ldraw4<T>(a.X, nb[k]);
+            ik[k] = ldraw4<T>(a.I, nb[k]);
+            vk[k] = ldraw4<T>(a.V, nb[k]);
         }
         const F4 pc = ld4<T>(a.P, ir);
         const F4 yv = ld4f(a.Y, ir), tv = ld4<T>(a.T, ir);  // output head h of this cell
@@ -269,17 +303,18 @@ __global__ __launch_bounds__(256) void bw_cell_kernel(BackwardArgs a) {
         for (int e = 0; e < 4; ++e) {
             float u = 0.f;
 #pragma unroll
-            for (int k = 0; k < 9; ++k) u = __builtin_fmaf(kw[k], xk[k].v[e], u);
+            for (int k = 0; k < 9; ++k) u = __builtin_fmaf(kw[k], raw_at<T>(xk[k], e), u);
             t[e] = (u - mu) * inv_sp;
             et[e] = __expf(-t[e] * t[e]);
             g[e] = 2.0f * et[e] - 1.0f;
         }
+        reuse_raw<T>(ik);
         float s[9], mx = -3.0e38f;
 #pragma unroll
         for (int k = 0; k < 9; ++k) {
             float d = 0.f;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) d = __builtin_fmaf(pc.v[e], ik[k].v[e], d);
+            for (int e = 0; e < 4; ++e) d = __builtin_fmaf(pc.v[e], raw_at<T>(ik[k], e), d);
             s[k] = lanes_sum<kL>(d) * inv_sqrt_d;
             mx = fmaxf(mx, s[k]);
         }
@@ -290,16 +325,17 @@ __global__ __launch_bounds__(256) void bw_cell_kernel(BackwardArgs a) {
             den += s[k];
         }
         const float rden = 1.0f / den;
+        reuse_raw<T>(vk);
         float vt[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int k = 0; k < 9; ++k) {
             s[k] *= rden;  // a_k
 #pragma unroll
-            for (int e = 0; e < 4; ++e) vt[e] = __builtin_fmaf(s[k], vk[k].v[e], vt[e]);
+            for (int e = 0; e < 4; ++e) vt[e] = __builtin_fmaf(s[k], raw_at<T>(vk[k], e), vt[e]);
         }
         float z[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) z[e] = __builtin_fmaf(dt * g[e], vt[e], xk[4].v[e]);
+        for (int e = 0; e < 4; ++e) z[e] = __builtin_fmaf(dt * g[e], vt[e], raw_at<T>(xk[4], e));
         // ---- S7 -> gY of output head h at (r, c0..c0+3), shared; S6 -> gZ_h ----
         {
             const float rs = a.scale[b * H + h];
@@ -315,11 +351,14 @@ __global__ __launch_bounds__(256) void bw_cell_kernel(BackwardArgs a) {
         for (int o = 0; o < H; ++o) {
             const float4 gq = *reinterpret_cast<const float4*>(sgy + cs * C + o * kD + c0);
             const float gy[4] = {gq.x, gq.y, gq.z, gq.w};
+            const float mo = mcol[o];
+            float pm = red[o][threadIdx.x];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                gz[e] = __builtin_fmaf(mcol[o], gy[e], gz[e]);
-                pM[o] = __builtin_fmaf(gy[e], z[e], pM[o]);
+                gz[e] = __builtin_fmaf(mo, gy[e], gz[e]);
+                pm = __builtin_fmaf(gy[e], z[e], pm);
             }
+            red[o][threadIdx.x] = pm;
         }
         __syncthreads();  // sgy is rewritten by the next iteration
         // ---- S6, S3 ----
@@ -339,30 +378,36 @@ __global__ __launch_bounds__(256) void bw_cell_kernel(BackwardArgs a) {
                 a.gcell[(r * H + h) * 2 + 1] = ssg;
             }
         } else {
-            pmu += gmu_l;
-            psg += gsg_l;
+            red[H + 9][threadIdx.x] += gmu_l;
+            red[H + 10][threadIdx.x] += gsg_l;
         }
+        reuse_raw<T>(xk);
 #pragma unroll
-        for (int k = 0; k < 9; ++k)
+        for (int k = 0; k < 9; ++k) {
+            float pk = red[H + k][threadIdx.x];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) pK[k] = __builtin_fmaf(gu[e], xk[k].v[e], pK[k]);
+            for (int e = 0; e < 4; ++e) pk = __builtin_fmaf(gu[e], raw_at<T>(xk[k], e), pk);
+            red[H + k][threadIdx.x] = pk;
+        }
         // ---- S5, S4 ----
+        reuse_raw<T>(vk);
         float ga[9], sa = 0.f;
 #pragma unroll
         for (int k = 0; k < 9; ++k) {
             float d = 0.f;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) d = __builtin_fmaf(gvt[e], vk[k].v[e], d);
+            for (int e = 0; e < 4; ++e) d = __builtin_fmaf(gvt[e], raw_at<T>(vk[k], e), d);
             ga[k] = lanes_sum<kL>(d);
             sa = __builtin_fmaf(s[k], ga[k], sa);
         }
+        reuse_raw<T>(ik);
         float gp[4] = {0.f, 0.f, 0.f, 0.f};
         float tape_a = 0.f, tape_gs = 0.f;  // kL >= 9: lane li < 9 holds a_li and gs_li
 #pragma unroll
         for (int k = 0; k < 9; ++k) {
             const float gs = s[k] * (ga[k] - sa);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) gp[e] = __builtin_fmaf(gs * inv_sqrt_d, ik[k].v[e], gp[e]);
+            for (int e = 0; e < 4; ++e) gp[e] = __builtin_fmaf(gs * inv_sqrt_d, raw_at<T>(ik[k], e), gp[e]);
             // the tape for the gathers: a_k and gs_k per (r, h)
             if constexpr (kL >= 9) {
                 tape_a = k == li ? s[k] : tape_a;
@@ -392,13 +437,6 @@ __global__ __launch_bounds__(256) void bw_cell_kernel(BackwardArgs a) {
         st4f(a.gXd, ir, gxd);
     }
     // block reduction of the parameter partials, fixed order
-    __shared__ float red[kPartF][256];
-#pragma unroll
-    for (int o = 0; o < H; ++o) red[o][threadIdx.x] = pM[o];
-#pragma unroll
-    for (int k = 0; k < 9; ++k) red[H + k][threadIdx.x] = pK[k];
-    red[H + 9][threadIdx.x] = pmu;
-    red[H + 10][threadIdx.x] = psg;
     __syncthreads();
     // per head h: the threads of groups g = cs * H + h, in the order (cs, lane)
     if ((int)threadIdx.x < H * kPartF) {
