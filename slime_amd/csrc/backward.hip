@@ -67,6 +67,12 @@ template <typename T>
 __device__ __forceinline__ Raw4<T> ldraw4(const void* p, long long i) {
     return *reinterpret_cast<const Raw4<T>*>(static_cast<const T*>(p) + i);
 }
+// Element `base` of p (a wave-uniform index), then `lane_bytes` further.
+template <typename T>
+__device__ __forceinline__ Raw4<T> ldraw4_at(const void* p, long long base, unsigned lane_bytes) {
+    const char* q = reinterpret_cast<const char*>(static_cast<const T*>(p) + base);
+    return *reinterpret_cast<const Raw4<T>*>(q + lane_bytes);
+}
 template <typename T>
 __device__ __forceinline__ float raw_at(const Raw4<T>& r, int e) {
     if constexpr (sizeof(T) == 2) {
@@ -232,7 +238,10 @@ void bw_cell_kernel(BackwardArgs a) {
     const long long cells = (long long)G * G;
     const int pod = blockIdx.x / a.nW;
     const int grp = threadIdx.x / kL, li = threadIdx.x % kL;
-    const int cs = grp / H, h = grp % H;
+    // When a cell's 8 heads fill whole waves (kD >= 32), the cell slot is the same in
+    // every lane of a wave; saying so moves the cell's index and neighbour arithmetic
+    // to the scalar unit.
+    const int cs = kL * H >= 64 ? __builtin_amdgcn_readfirstlane(grp / H) : grp / H, h = grp % H;
     const int c0 = 4 * li;
     // pod_cells is a multiple of kCpi (G is a multiple of 8, kCpi <= 16), so every slot
     // of an iteration is a cell and all threads of the block run the same iterations
@@ -273,18 +282,20 @@ void bw_cell_kernel(BackwardArgs a) {
         const int y = (int)(cell / G), x = (int)(cell % G);
         const long long r = (long long)b * cells + cell;
         const long long ir = r * C + h * kD + c0;
+        // Neighbour k's first element, and this lane's channels within a cell: a
+        // wave-uniform base and a 32-bit lane offset per load.
+        const unsigned lane_b = (unsigned)((h * kD + c0) * sizeof(T));
         long long nb[9];
 #pragma unroll
         for (int k = 0; k < 9; ++k)
-            nb[k] = ((long long)b * cells + (long long)wrapb(y + k / 3 - 1, G) * G + wrapb(x + k % 3 - 1, G)) * C +
-                    h * kD + c0;
+            nb[k] = ((long long)b * cells + (long long)wrapb(y + k / 3 - 1, G) * G + wrapb(x + k % 3 - 1, G)) * C;
         // ---- forward locals of head h at r (4 channels) ----
         Raw4<T> xk[9], ik[9], vk[9];
 #pragma unroll
         for (int k = 0; k < 9; ++k) {
-            xk[k] = ldraw4<T>(a.X, nb[k]);
-            ik[k] = ldraw4<T>(a.I, nb[k]);
-            vk[k] = ldraw4<T>(a.V, nb[k]);
+            xk[k] = ldraw4_at<T>(a.X, nb[k], lane_b);
+            ik[k] = ldraw4_at<T>(a.I, nb[k], lane_b);
+            vk[k] = ldraw4_at<T>(a.V, nb[k], lane_b);
         }
         const F4 pc = ld4<T>(a.P, ir);
         const F4 yv = ld4f(a.Y, ir), tv = ld4<T>(a.T, ir);  // output head h of this cell
