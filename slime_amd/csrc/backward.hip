@@ -859,6 +859,103 @@ __global__ __launch_bounds__(256) void bw_dw_mfma_kernel(BackwardArgs a, DwArgs 
             }
 }
 
+// bf16 with C a multiple of 256: 256 x 256 output tiles, wave (wk, wj) owning
+// 128 x 128 as 8 x 8 v_mfma_f32_16x16x32_bf16 blocks, so each staged byte feeds twice
+// the matrix work of the 128-column tiles above. Each operand's 256 columns are staged
+// as two [32 rows][128 columns] sub-tiles in the layout above, so the direct loads and
+// the transposing reads are those of bw_dw_mfma_kernel plus a sub-tile offset; every
+// output sums the same rows with the same instructions in the same order.
+constexpr int kDw2T = 2 * kDwT, kDw2SubB = kDwStep * kDwRowB;  // 8 KiB per sub-tile
+constexpr int kDw2StageB = 4 * kDw2SubB;                        // X0 X1 G0 G1: 32 KiB
+constexpr int kDw2Stages = 4;                                   // 128 KiB
+
+__global__ __launch_bounds__(256) void bw_dw_mfma2_kernel(BackwardArgs a, DwArgs d) {
+    __shared__ __attribute__((aligned(1024))) unsigned char lds[kDw2Stages * kDw2StageB];
+    const int C = d.C, N3 = 3 * C;
+    const int kt = blockIdx.x, jt = blockIdx.y, chunk = blockIdx.z;
+    const int pod = chunk / d.chunks_per_pod;
+    const long long r0 = (long long)pod * d.rows_per_pod + (long long)(chunk % d.chunks_per_pod) * d.rows_per_chunk;
+    const long long r1 = min(r0 + d.rows_per_chunk, (long long)(pod + 1) * d.rows_per_pod);
+    const int nsteps = (int)((r1 - r0) / kDwStep);  // rows are a multiple of kDwStep (host-checked)
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wk = wave & 1, wj = wave >> 1;
+    const char* Xs = reinterpret_cast<const char*>(static_cast<const bf16_t*>(a.X) + r0 * C + (long long)kt * kDw2T);
+    const char* Gs = reinterpret_cast<const char*>(static_cast<const bf16_t*>(a.G3) + r0 * N3 + (long long)jt * kDw2T);
+    const int drow = lane >> 4, dchunk = (lane & 15) ^ (2 * drow);
+    const unsigned xoff = (unsigned)(drow * C * 2 + dchunk * 16), goff = (unsigned)(drow * N3 * 2 + dchunk * 16);
+    auto issue = [&](int st, int stage) {  // step st (clamped: past the end refetch the last)
+        const long long rb = (long long)(st < nsteps ? st : nsteps - 1) * kDwStep;
+        const unsigned sb = (unsigned)(size_t)(const dw_lds_void*)(lds + stage * kDw2StageB);
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int q = 2 * wave + u;
+                dw_dma16(Xs + (rb + 4 * q) * C * 2 + sub * kDwRowB, xoff, sb + sub * kDw2SubB + q * 1024);
+                dw_dma16(Gs + (rb + 4 * q) * N3 * 2 + sub * kDwRowB, goff, sb + (2 + sub) * kDw2SubB + q * 1024);
+            }
+    };
+    // operand reads: as in bw_dw_mfma_kernel; blocks b and b + 4 differ by 8 chunks
+    // (128 bytes), which the chunk swizzle (bits 1-2 of the chunk) leaves alone
+    const int g = lane >> 4, i = lane & 15;
+    auto rd = [&](int col0, int hf) {
+        const int row = 8 * g + 4 * hf + (i >> 2);
+        const int chunk_l = col0 / 8 + ((i & 3) >> 1);
+        return row * kDwRowB + ((chunk_l ^ (2 * (i >> 2))) << 4) + 8 * (i & 1);
+    };
+    int roff[2][4][2];  // [x/g][block & 3][hf], with the wave's sub-tile offset
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+            roff[0][b][hf] = wk * kDw2SubB + rd(b * 16, hf);
+            roff[1][b][hf] = (2 + wj) * kDw2SubB + rd(b * 16, hf);
+        }
+    f32x4 acc[8][8];
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb)
+#pragma unroll
+        for (int jb = 0; jb < 8; ++jb) acc[kb][jb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (nsteps > 0) {
+#pragma unroll
+        for (int st = 0; st < kDw2Stages - 1; ++st) issue(st, st);
+    }
+    for (int st = 0; st < nsteps; ++st) {
+        dw_wait<8 * (kDw2Stages - 2)>();  // this wave's loads of step st have landed
+        dw_barrier();                     // ... and every wave's; step st-1's stage is free
+        issue(st + kDw2Stages - 1, (st + kDw2Stages - 1) % kDw2Stages);
+        const unsigned char* base = lds + (st % kDw2Stages) * kDw2StageB;
+        uint4 av[8], bv[8];
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            const int hi = (b >> 2) * 128;
+            const uint2 x0 = dw_tr16(base + roff[0][b & 3][0] + hi), x1 = dw_tr16(base + roff[0][b & 3][1] + hi);
+            const uint2 g0 = dw_tr16(base + roff[1][b & 3][0] + hi), g1 = dw_tr16(base + roff[1][b & 3][1] + hi);
+            av[b] = make_uint4(x0.x, x0.y, x1.x, x1.y);
+            bv[b] = make_uint4(g0.x, g0.y, g1.x, g1.y);
+        }
+#pragma unroll
+        for (int kb = 0; kb < 8; ++kb)
+#pragma unroll
+            for (int jb = 0; jb < 8; ++jb)
+                acc[kb][jb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    __builtin_bit_cast(bf16x8_v, av[kb]), __builtin_bit_cast(bf16x8_v, bv[jb]), acc[kb][jb], 0, 0, 0);
+    }
+    dw_wait<0>();  // refetched steps may still be landing in LDS
+    float* out = d.part + (long long)chunk * C * N3;
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb)
+#pragma unroll
+        for (int jb = 0; jb < 8; ++jb)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int k = kt * kDw2T + wk * 128 + kb * 16 + 4 * g + e;
+                const int j = jt * kDw2T + wj * 128 + jb * 16 + i;
+                out[(long long)k * N3 + j] = acc[kb][jb][e];
+            }
+}
+
 __global__ __launch_bounds__(256) void bw_dw_reduce_kernel(DwArgs d) {
     const int C = d.C, N3 = 3 * C;
     const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;  // (pod, k, j)
@@ -944,7 +1041,10 @@ hipError_t launch_backward_stencil(int dtype, const BackwardArgs& a, hipStream_t
 
 hipError_t launch_backward_dw(int dtype, const BackwardArgs& a, const DwArgs& d, hipStream_t s) {
     const dim3 grid(d.C / 64, 3 * d.C / 64, d.pods * d.chunks_per_pod);
-    if (dw_mfma(dtype, d.C, d.rows_per_pod))
+    if (dw_mfma(dtype, d.C, d.rows_per_pod) && d.C % kDw2T == 0)
+        hipLaunchKernelGGL(bw_dw_mfma2_kernel, dim3(d.C / kDw2T, 3 * d.C / kDw2T, d.pods * d.chunks_per_pod),
+                           dim3(256), 0, s, a, d);
+    else if (dw_mfma(dtype, d.C, d.rows_per_pod))
         hipLaunchKernelGGL(bw_dw_mfma_kernel, dim3(d.C / kDwT, 3 * d.C / kDwT, d.pods * d.chunks_per_pod),
                            dim3(256), 0, s, a, d);
     else if (dtype == 1)
