@@ -14,6 +14,7 @@
 //   * sqrt_ge1(x): Goldschmidt's coupled iteration g -> sqrt(x), h -> 1/(2 sqrt x)
 //     from y = rsq(x), then two residual corrections g += (x - g^2) h. Needs
 //     1 <= x < 2^900, where no pre-scale applies.
+//   * rcp_sqrt_ge1(x): 1 / sqrt(x) with both roundings, from the same iteration.
 // slime_probe_fp64_core (probe.hip) checks both against `/` and `sqrt` bit for
 // bit over the rotation's operand ranges on the device.
 #pragma once
@@ -40,6 +41,24 @@ __device__ __forceinline__ double sqrt_ge1(double x) {
     return __builtin_fma(__builtin_fma(-g, g, x), h, g);
 }
 
+// rcp_sqrt_ge1(x) = 1 / sqrt(x) with both IEEE roundings (the bits of `1.0 / sqrt(x)`),
+// 1 <= x < 2^900: sqrt_ge1's g, then the reciprocal of g from 2 h (h approximates
+// 1 / (2 sqrt x) to ~2^-44 after the coupled step) by one Newton-Raphson step and
+// the same correction as div_rn with a = 1. This replaces the v_rcp_f64 and one of
+// the two refinement steps that div_rn(1, sqrt_ge1(x)) takes.
+__device__ __forceinline__ double rcp_sqrt_ge1(double x) {
+    const double y = __builtin_amdgcn_rsq(x);
+    double g = x * y, h = 0.5 * y;
+    const double e = __builtin_fma(-h, g, 0.5);
+    g = __builtin_fma(g, e, g);
+    h = __builtin_fma(h, e, h);
+    g = __builtin_fma(__builtin_fma(-g, g, x), h, g);
+    g = __builtin_fma(__builtin_fma(-g, g, x), h, g);
+    double r = 2.0 * h;
+    r = __builtin_fma(r, __builtin_fma(-g, r, 1.0), r);
+    return __builtin_fma(__builtin_fma(-g, r, 1.0), r, r);
+}
+
 // The rotation of the cyclic Jacobi solve for the 2x2 block [[app, apq], [apq, aqq]],
 // |apq| > 0: tau = (aqq - app) / (2 apq), t = sign(tau) / (|tau| + sqrt(1 + tau^2))
 // (t = +1 at tau = +-0), c = 1 / sqrt(1 + t^2), s = t c. |t| <= 1, so the second
@@ -53,7 +72,7 @@ __device__ __forceinline__ void jacobi_rotation(double app, double aqq, double a
         const double tau = div_rn(aqq - app, 2.0 * apq);
         const double u = div_rn(1.0, fabs(tau) + sqrt_ge1(1.0 + tau * tau));
         const double t = tau < 0.0 ? -u : u;
-        c = div_rn(1.0, sqrt_ge1(1.0 + t * t));
+        c = rcp_sqrt_ge1(1.0 + t * t);
         s = t * c;
     } else {
         const double tau = (aqq - app) / (2.0 * apq);

@@ -106,8 +106,8 @@ __device__ double draw(uint64_t r, int lo, int hi, bool sign) {
     return __builtin_bit_cast(double, bits);
 }
 
-// Per index i: div_rn against / on (a, b) with exponents in [-60, 60], sqrt_ge1
-// against sqrt on x in [1, 2^120), and the whole rotation (c, s) against its IEEE
+// Per index i: div_rn against / on (a, b) with exponents in [-60, 60], sqrt_ge1 and
+// rcp_sqrt_ge1 against sqrt and 1 / sqrt on x in [1, 2^120), and the whole rotation (c, s) against its IEEE
 // form on (app, aqq, apq) drawn like Gram entries, every eighth with app = aqq.
 __global__ void fp64_core_check(long long n, uint64_t seed, unsigned long long* bad) {
     unsigned long long miss = 0;
@@ -118,6 +118,7 @@ __global__ void fp64_core_check(long long n, uint64_t seed, unsigned long long* 
         if (__builtin_bit_cast(uint64_t, slime::div_rn(a, b)) != __builtin_bit_cast(uint64_t, a / b)) ++miss;
         const double x = draw(r2, 0, 119, false);
         if (__builtin_bit_cast(uint64_t, slime::sqrt_ge1(x)) != __builtin_bit_cast(uint64_t, sqrt(x))) ++miss;
+        if (__builtin_bit_cast(uint64_t, slime::rcp_sqrt_ge1(x)) != __builtin_bit_cast(uint64_t, 1.0 / sqrt(x))) ++miss;
         const double app = draw(r0 ^ r3, -24, 8, false);
         const double aqq = (i % 8 == 0) ? app : draw(r1 ^ r3, -24, 8, false);
         const double apq = draw(r2 ^ (r3 << 7), -19, 8, true);  // |apq| > 1e-6 as in the solve

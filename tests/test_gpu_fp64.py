@@ -28,4 +28,4 @@ def _probe():
 def test_short_fp64_forms_equal_ieee(seed):
     print(f"[case] fp64 core check seed={seed}", flush=True)
     bad = _probe().slime_probe_fp64_core(1 << 22, seed)
-    assert bad == 0, f"{bad} mismatches in {3 << 22} comparisons"
+    assert bad == 0, f"{bad} mismatches in {4 << 22} comparisons"
