@@ -309,6 +309,10 @@ __global__ __launch_bounds__(64) void fitness_finalize_kernel(FitnessArgs f) {
         for (int p = 0; p < D - 1; ++p) {
             lds_order();
             double colp = own ? A[lane * kLd + p] : 0.0;  // A[lane][p] = a_p,lane
+            // The read has landed before the rotations start; without this the loop
+            // head waits for every LDS access in flight, the previous rotation's
+            // writes included, on each rotation.
+            asm volatile("" : "+v"(colp));
             double app = lane_f64(diag, p);
             for (int q = p + 1;;) {
                 // Pairs (p, q..) with |a_pq| <= tol are skipped without changing anything,
