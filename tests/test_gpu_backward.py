@@ -164,6 +164,38 @@ class _LocalStep:
         return far + near
 
 
+@pytest.mark.parametrize("G", [128, 136])
+def test_weight_gradients_over_several_row_chunks(G):
+    """bf16, D = 64, a batch of 2 on a G^2 grid: 2 G^2 rows per pod, so the weight
+    gradients run as several 16,384-row chunks on the 256 x 256 tiles, added in chunk
+    order (G = 136 leaves a partial last chunk). The loss is a mean over the batch and
+    the mass rescale is per (batch entry, head), so every parameter gradient of the
+    batch is half the sum of the single-entry ones (one or two chunks each), and the
+    batch's dL/dX at entry i is half that entry's own."""
+    cfg = _cfg(B=2, G=G, D=64, dtype="bf16")
+    print(f"[case] backward over row chunks bf16 D64 B2 G{G}", flush=True)
+    p, X, T = _inputs(cfg)
+
+    def grads(Xb, Tb):
+        with Pseudopod(Xb.shape[0], G, 8, 64, "bf16", cfg.dt, False, 1) as e:
+            e.set_params(p)
+            loss, gx, g = e.backward(_dev(Xb, "bf16"), _dev(Tb, "bf16"))
+            torch.cuda.synchronize()
+            return loss, gx.cpu().numpy(), {k: v.cpu().numpy().astype(np.float64) for k, v in g.items()}
+
+    loss2, gx2, g2 = grads(X, T)
+    parts = [grads(X[i:i + 1], T[i:i + 1]) for i in range(2)]
+    assert abs(loss2 - 0.5 * (parts[0][0] + parts[1][0])) <= 1e-9 * loss2
+    for k in NAMES:
+        err = norm_err(g2[k], 0.5 * (parts[0][2][k] + parts[1][2][k]))
+        print(f"  {k}: normalised error {err:.2e}")
+        assert err <= 1e-5, (k, err)
+    for i in range(2):
+        err = norm_err(gx2[i], 0.5 * parts[i][1][0])
+        print(f"  dX entry {i}: normalised error {err:.2e}")
+        assert err <= 1e-5
+
+
 def test_c5_gradient_matches_finite_differences_on_64_cells():
     from slime_amd import CONFIGS
     cfg = CONFIGS["c5"]
