@@ -864,7 +864,10 @@ __global__ __launch_bounds__(256) void bw_dw_mfma_kernel(BackwardArgs a, DwArgs 
 // the matrix work of the 128-column tiles above. Each operand's 256 columns are staged
 // as two [32 rows][128 columns] sub-tiles in the layout above, so the direct loads and
 // the transposing reads are those of bw_dw_mfma_kernel plus a sub-tile offset; every
-// output sums the same rows with the same instructions in the same order.
+// output sums the same rows with the same instructions in the same order. One more
+// swizzle bit keeps the 16-lane groups of a transposing read, whose rows are 8 apart
+// (a whole number of bank sweeps), on different banks: chunk bit 3 flips in rows
+// 8 .. 15 of every 16 (2.0 bank-conflict cycles per LDS read without it).
 constexpr int kDw2T = 2 * kDwT, kDw2SubB = kDwStep * kDwRowB;  // 8 KiB per sub-tile
 constexpr int kDw2StageB = 4 * kDw2SubB;                        // X0 X1 G0 G1: 32 KiB
 constexpr int kDw2Stages = 4;                                   // 128 KiB
@@ -882,8 +885,13 @@ __global__ __launch_bounds__(256) void bw_dw_mfma2_kernel(BackwardArgs a, DwArgs
     const int wk = wave & 1, wj = wave >> 1;
     const char* Xs = reinterpret_cast<const char*>(static_cast<const bf16_t*>(a.X) + r0 * C + (long long)kt * kDw2T);
     const char* Gs = reinterpret_cast<const char*>(static_cast<const bf16_t*>(a.G3) + r0 * N3 + (long long)jt * kDw2T);
-    const int drow = lane >> 4, dchunk = (lane & 15) ^ (2 * drow);
-    const unsigned xoff = (unsigned)(drow * C * 2 + dchunk * 16), goff = (unsigned)(drow * N3 * 2 + dchunk * 16);
+    // Rows 8 .. 15 of every 16 (instructions q with q / 2 odd, i.e. odd waves) also flip
+    // chunk bit 3.
+    const int drow = lane >> 4;
+    const int dchunk0 = (lane & 15) ^ (2 * drow), dchunk1 = dchunk0 ^ 8;
+    const unsigned xoff0 = (unsigned)(drow * C * 2 + dchunk0 * 16), goff0 = (unsigned)(drow * N3 * 2 + dchunk0 * 16);
+    const unsigned xoff1 = (unsigned)(drow * C * 2 + dchunk1 * 16), goff1 = (unsigned)(drow * N3 * 2 + dchunk1 * 16);
+    const unsigned xoff = (wave & 1) ? xoff1 : xoff0, goff = (wave & 1) ? goff1 : goff0;
     auto issue = [&](int st, int stage) {  // step st (clamped: past the end refetch the last)
         const long long rb = (long long)(st < nsteps ? st : nsteps - 1) * kDwStep;
         const unsigned sb = (unsigned)(size_t)(const dw_lds_void*)(lds + stage * kDw2StageB);
@@ -896,17 +904,17 @@ __global__ __launch_bounds__(256) void bw_dw_mfma2_kernel(BackwardArgs a, DwArgs
                 dw_dma16(Gs + (rb + 4 * q) * N3 * 2 + sub * kDwRowB, goff, sb + (2 + sub) * kDw2SubB + q * 1024);
             }
     };
-    // operand reads: as in bw_dw_mfma_kernel; blocks b and b + 4 differ by 8 chunks
-    // (128 bytes), which the chunk swizzle (bits 1-2 of the chunk) leaves alone
+    // operand reads: as in bw_dw_mfma_kernel, with the chunk's bit 3 flipped in rows
+    // 8 .. 15 of every 16 (16-lane group g reads rows 8 g .. 8 g + 7)
     const int g = lane >> 4, i = lane & 15;
     auto rd = [&](int col0, int hf) {
         const int row = 8 * g + 4 * hf + (i >> 2);
         const int chunk_l = col0 / 8 + ((i & 3) >> 1);
-        return row * kDwRowB + ((chunk_l ^ (2 * (i >> 2))) << 4) + 8 * (i & 1);
+        return row * kDwRowB + ((chunk_l ^ (2 * (i >> 2)) ^ (8 * (g & 1))) << 4) + 8 * (i & 1);
     };
-    int roff[2][4][2];  // [x/g][block & 3][hf], with the wave's sub-tile offset
+    int roff[2][8][2];  // [x/g][block][hf], with the wave's sub-tile offset
 #pragma unroll
-    for (int b = 0; b < 4; ++b)
+    for (int b = 0; b < 8; ++b)
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf) {
             roff[0][b][hf] = wk * kDw2SubB + rd(b * 16, hf);
@@ -929,9 +937,8 @@ __global__ __launch_bounds__(256) void bw_dw_mfma2_kernel(BackwardArgs a, DwArgs
         uint4 av[8], bv[8];
 #pragma unroll
         for (int b = 0; b < 8; ++b) {
-            const int hi = (b >> 2) * 128;
-            const uint2 x0 = dw_tr16(base + roff[0][b & 3][0] + hi), x1 = dw_tr16(base + roff[0][b & 3][1] + hi);
-            const uint2 g0 = dw_tr16(base + roff[1][b & 3][0] + hi), g1 = dw_tr16(base + roff[1][b & 3][1] + hi);
+            const uint2 x0 = dw_tr16(base + roff[0][b][0]), x1 = dw_tr16(base + roff[0][b][1]);
+            const uint2 g0 = dw_tr16(base + roff[1][b][0]), g1 = dw_tr16(base + roff[1][b][1]);
             av[b] = make_uint4(x0.x, x0.y, x1.x, x1.y);
             bv[b] = make_uint4(g0.x, g0.y, g1.x, g1.y);
         }
