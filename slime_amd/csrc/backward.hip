@@ -734,7 +734,8 @@ __global__ __launch_bounds__(256) void bw_dw_partial_kernel(BackwardArgs a, DwAr
 // 16-lane group, lane j reads 4 columns of row rbase + j / 4, and lane i then holds
 // column i of rows rbase .. rbase + 3, the MFMA operand layout (8 consecutive rows
 // of one column per lane, two reads). The 16-byte chunks of row r sit at chunk ^
-// 2 (r % 4), so the four rows of a read fall in disjoint banks.
+// 2 (r % 4) ^ 8 ((r / 8) % 2): the four rows of a 16-lane group's read fall in
+// disjoint banks, and so do the groups, whose rows are 8 apart.
 constexpr int kDwT = 128, kDwStep = 32, kDwRowB = 2 * kDwT, kDwStages = 4;
 constexpr int kDwStageB = 2 * kDwStep * kDwRowB;  // X and G tiles, 16 KiB
 constexpr long long kDwRowsMfma = 16384;
@@ -788,7 +789,8 @@ __global__ __launch_bounds__(256) void bw_dw_mfma_kernel(BackwardArgs a, DwArgs 
     // Direct loads: instruction q of a tile fills rows 4 q .. 4 q + 3; lane l lands in
     // row l / 16 of those, physical chunk l % 16, fetching logical chunk
     // (l % 16) ^ 2 (l / 16). Wave w issues instructions 2 w and 2 w + 1 of each tile.
-    const int drow = lane >> 4, dchunk = (lane & 15) ^ (2 * drow);
+    // Odd waves fill rows 8 .. 15 of every 16, whose chunk bit 3 is also flipped.
+    const int drow = lane >> 4, dchunk = (lane & 15) ^ (2 * drow) ^ (8 * (wave & 1));
     const unsigned xoff = (unsigned)(drow * C * 2 + dchunk * 16), goff = (unsigned)(drow * N3 * 2 + dchunk * 16);
     auto issue = [&](int st, int stage) {  // step st (clamped: past the end refetch the last)
         const long long rb = (long long)(st < nsteps ? st : nsteps - 1) * kDwStep;
@@ -805,7 +807,7 @@ __global__ __launch_bounds__(256) void bw_dw_mfma_kernel(BackwardArgs a, DwArgs 
     auto rd = [&](int col0, int hf) {  // byte offset of this lane's 8 bytes in a tile
         const int row = 8 * g + 4 * hf + (i >> 2);
         const int chunk_l = col0 / 8 + ((i & 3) >> 1);
-        return row * kDwRowB + ((chunk_l ^ (2 * (i >> 2))) << 4) + 8 * (i & 1);
+        return row * kDwRowB + ((chunk_l ^ (2 * (i >> 2)) ^ (8 * (g & 1))) << 4) + 8 * (i & 1);
     };
     int roff[2][4][2];  // [x/g][block][hf]
 #pragma unroll
@@ -864,10 +866,9 @@ __global__ __launch_bounds__(256) void bw_dw_mfma_kernel(BackwardArgs a, DwArgs 
 // the matrix work of the 128-column tiles above. Each operand's 256 columns are staged
 // as two [32 rows][128 columns] sub-tiles in the layout above, so the direct loads and
 // the transposing reads are those of bw_dw_mfma_kernel plus a sub-tile offset; every
-// output sums the same rows with the same instructions in the same order. One more
-// swizzle bit keeps the 16-lane groups of a transposing read, whose rows are 8 apart
-// (a whole number of bank sweeps), on different banks: chunk bit 3 flips in rows
-// 8 .. 15 of every 16 (2.0 bank-conflict cycles per LDS read without it).
+// output sums the same rows with the same instructions in the same order. (Without
+// the swizzle's bit 3, the 16-lane groups of a read, rows 8 apart, shared banks: 2.0
+// conflict cycles per LDS read.)
 constexpr int kDw2T = 2 * kDwT, kDw2SubB = kDwStep * kDwRowB;  // 8 KiB per sub-tile
 constexpr int kDw2StageB = 4 * kDw2SubB;                        // X0 X1 G0 G1: 32 KiB
 constexpr int kDw2Stages = 4;                                   // 128 KiB
@@ -885,13 +886,9 @@ __global__ __launch_bounds__(256) void bw_dw_mfma2_kernel(BackwardArgs a, DwArgs
     const int wk = wave & 1, wj = wave >> 1;
     const char* Xs = reinterpret_cast<const char*>(static_cast<const bf16_t*>(a.X) + r0 * C + (long long)kt * kDw2T);
     const char* Gs = reinterpret_cast<const char*>(static_cast<const bf16_t*>(a.G3) + r0 * N3 + (long long)jt * kDw2T);
-    // Rows 8 .. 15 of every 16 (instructions q with q / 2 odd, i.e. odd waves) also flip
-    // chunk bit 3.
-    const int drow = lane >> 4;
-    const int dchunk0 = (lane & 15) ^ (2 * drow), dchunk1 = dchunk0 ^ 8;
-    const unsigned xoff0 = (unsigned)(drow * C * 2 + dchunk0 * 16), goff0 = (unsigned)(drow * N3 * 2 + dchunk0 * 16);
-    const unsigned xoff1 = (unsigned)(drow * C * 2 + dchunk1 * 16), goff1 = (unsigned)(drow * N3 * 2 + dchunk1 * 16);
-    const unsigned xoff = (wave & 1) ? xoff1 : xoff0, goff = (wave & 1) ? goff1 : goff0;
+    // Odd waves fill rows 8 .. 15 of every 16, whose chunk bit 3 is also flipped.
+    const int drow = lane >> 4, dchunk = (lane & 15) ^ (2 * drow) ^ (8 * (wave & 1));
+    const unsigned xoff = (unsigned)(drow * C * 2 + dchunk * 16), goff = (unsigned)(drow * N3 * 2 + dchunk * 16);
     auto issue = [&](int st, int stage) {  // step st (clamped: past the end refetch the last)
         const long long rb = (long long)(st < nsteps ? st : nsteps - 1) * kDwStep;
         const unsigned sb = (unsigned)(size_t)(const dw_lds_void*)(lds + stage * kDw2StageB);
@@ -904,8 +901,7 @@ __global__ __launch_bounds__(256) void bw_dw_mfma2_kernel(BackwardArgs a, DwArgs
                 dw_dma16(Gs + (rb + 4 * q) * N3 * 2 + sub * kDwRowB, goff, sb + (2 + sub) * kDw2SubB + q * 1024);
             }
     };
-    // operand reads: as in bw_dw_mfma_kernel, with the chunk's bit 3 flipped in rows
-    // 8 .. 15 of every 16 (16-lane group g reads rows 8 g .. 8 g + 7)
+    // operand reads: as in bw_dw_mfma_kernel (16-lane group g reads rows 8 g .. 8 g + 7)
     const int g = lane >> 4, i = lane & 15;
     auto rd = [&](int col0, int hf) {
         const int row = 8 * g + 4 * hf + (i >> 2);

@@ -53,6 +53,8 @@ def _dev(a, dtype):
     ("bf16", 64, 2, True, 2, 16),
     # C = 256: one wave per cell in the cell pass, one 256-column tile per operand in dW
     ("bf16", 32, 2, False, 2, 16),
+    # C = 128: the 128 x 128 weight-gradient tiles
+    ("bf16", 16, 1, True, 2, 16),
     # the smallest grid: 64 cells per pod, fewer than 8 whole cell-pass iterations
     ("fp32", 8, 1, False, 1, 8),
     ("fp32", 8, 3, True, 3, 8),
