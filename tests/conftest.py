@@ -26,3 +26,26 @@ def oracle():
     import oracle as o
     o.build()
     return o
+
+
+# Weight scales of the peaked-attention parity cases. At the configurations' own
+# N(0, 0.05) weights the local softmax is nearly uniform (largest weight ~0.16
+# against 1/9) and the value term dt*g*V~ is small beside X, so a wrong attention
+# (uniform, mirrored neighbours, query and key swapped) moves Y by less than the
+# bf16 bar of 2e-2. With W_P, W_I ~ N(0, 0.25) the largest weight of a cell
+# averages ~0.63, and with W_V ~ N(0, 0.15) the propagated value is a visible
+# share of Y: the same mistakes then move Y by 0.18-0.39.
+PEAKED_QK_STD = 0.25
+PEAKED_V_STD = 0.15
+
+
+def peaked_params(cfg, seed=1):
+    """make_params(cfg, seed) with W_P, W_I ~ N(0, PEAKED_QK_STD) and W_V ~
+    N(0, PEAKED_V_STD), drawn from a second stream seeded with seed + 1000;
+    K, M, mu and sigma are those of make_params."""
+    from slime_amd import make_params
+    p = make_params(cfg, seed=seed)
+    rng = np.random.default_rng(seed + 1000)
+    for k, s in (("WP", PEAKED_QK_STD), ("WI", PEAKED_QK_STD), ("WV", PEAKED_V_STD)):
+        p[k] = rng.normal(0.0, s, p[k].shape).astype(np.float32)
+    return p

@@ -142,6 +142,67 @@ def test_flow_lenia_matches_oracle_on_same_projections(oracle, dtype):
     assert np.all(drift <= bound * np.abs(rmi)), drift / np.abs(rmi)
 
 
+# ---- peaked attention: the bf16 matrix-core stencil's S4 and S5 ------------------------------
+#
+# At the configurations' own weights the attention is nearly uniform and the tests
+# above cannot see S4/S5 (a uniform, mirrored or query/key-swapped attention moves Y
+# by less than the bf16 bar). These cases use the peaked weights of
+# tests.conftest.peaked_params, where tests/test_oracle.py shows on the same inputs
+# that each of those mistakes moves Y by more than 5x the bar.
+
+def _prep_peaked(cfg, pseed=1, sseed=2):
+    from tests.conftest import peaked_params
+    p = peaked_params(cfg, seed=pseed)
+    p = {k: (round_bf16(v) if k in ("WP", "WI", "WV") else v) for k, v in p.items()}
+    return p, round_bf16(make_state(cfg, seed=sseed))
+
+
+@pytest.mark.parametrize("G", [16, 32])
+def test_flow_lenia_peaked_attention_matches_oracle_on_same_projections(oracle, G):
+    cfg = _cfg("peak", B=2, G=G, D=64, dtype="bf16", pods=2)
+    p, X = _prep_peaked(cfg)
+    with _engine(cfg) as e:
+        assert e.uses_mfma
+        e.set_params(p)
+        x = _dev(X, "bf16")
+        P, I, V = e.project(x)
+        y = e.flow_lenia(x, P, I, V)
+        torch.cuda.synchronize()
+        mi, mo = e.mass()
+        hp, hi, hv, Y = (_host(t) for t in (P, I, V, y))
+    ocfg = _ocfg(cfg)
+    A = oracle.attention(ocfg, hp, hi)
+    peak = float(A.max(axis=-1).mean())
+    ref, rmi, _ = _oracle_flow(oracle, ocfg, X, hp, hi, hv, p)
+    err = norm_err(Y, ref)
+    print(f"  G={G}: mean largest attention weight {peak:.3f}; Y normalised error {err:.3e}")
+    assert peak > 0.5  # the case is peaked, or it pins nothing
+    assert err <= TOL["bf16"]
+    np.testing.assert_allclose(mi, rmi, rtol=1e-6)
+    np.testing.assert_allclose(mo, mi, rtol=1e-6)
+
+
+@pytest.mark.parametrize("per_cell", [False, True])
+def test_step_peaked_attention_matches_oracle(oracle, per_cell):
+    # The whole step against the oracle's own projections: the device's bf16-rounded
+    # P and I move the scores by ~0.4 % of their size, which flips no neighbour
+    # choice at these seeds (a flip would show as an error of ~0.1).
+    cfg = _cfg("peakstep", B=2, G=16, D=64, dtype="bf16", pods=2, growth_per_cell=per_cell)
+    p, X = _prep_peaked(cfg)
+    with _engine(cfg) as e:
+        e.set_params(p)
+        y = e.forward(_dev(X, "bf16"))
+        torch.cuda.synchronize()
+        mi, mo = e.mass()
+        Y = _host(y)
+    ref, rmi, _ = oracle.step(_ocfg(cfg), X, p, 1)
+    err = norm_err(Y, ref)
+    print(f"  Y: normalised error {err:.3e}")
+    assert err <= TOL["bf16"]
+    np.testing.assert_allclose(mi, rmi, rtol=1e-6)
+    np.testing.assert_allclose(mo, mi, rtol=1e-6)
+
+
 # ---- full steps ------------------------------------------------------------------------------
 
 @pytest.mark.parametrize("dtype,per_cell,pods,chain,D", [

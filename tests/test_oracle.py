@@ -205,6 +205,55 @@ def test_attention_matches_vectorised_numpy(oracle):
     np.testing.assert_allclose(A, e / e.sum(-1, keepdims=True), rtol=1e-5, atol=1e-7)
 
 
+@pytest.mark.parametrize("G", [16, 32])
+def test_peaked_attention_case_sees_planted_s4_s5_mistakes(oracle, G):
+    """The inputs of the GPU peaked-attention parity cases (bf16 D=64, 2 pods,
+    tests.conftest.peaked_params), run through the oracle with one stage mistake
+    planted at a time. Each moves Y by more than 5x the bf16 bar of 2e-2, while the
+    rounding the device applies (bf16 P, I, V, attention weights and Y) moves it
+    by less than a quarter of the bar: a device with any of these mistakes fails
+    the GPU cases, and a correct one passes them."""
+    from slime_amd import make_state, round_bf16
+    from slime_amd.synthetic import CAConfig
+    from tests.conftest import peaked_params
+    bar = 2e-2
+    scfg = CAConfig("peak", B=2, G=G, H=H, D=64, dtype="bf16", steps=1, w_std=0.05, pods=2)
+    p = peaked_params(scfg)
+    p = {k: (round_bf16(v) if k in ("WP", "WI", "WV") else v) for k, v in p.items()}
+    X = round_bf16(make_state(scfg, seed=2))
+    cfg = OracleConfig(B=2, G=G, H=H, D=64, pods=2)
+    P, I, V = map(round_bf16, oracle.project(cfg, X, p["WP"], p["WI"], p["WV"]))
+    g = oracle.growth(cfg, oracle.potential(cfg, X, p["K"]), p["mu"], p["sigma"])
+
+    def y_of(A):
+        Y = oracle.mix(cfg, X, g, oracle.propagate(cfg, A, V), p["M"])
+        return oracle.conserve(cfg, X, Y)[0]
+
+    A = oracle.attention(cfg, P, I)
+    assert A.max(axis=-1).mean() > 0.5
+    Y = y_of(A)
+    centre = np.zeros_like(A)
+    centre[..., 4] = 1.0
+    planted = {
+        "uniform attention": np.full_like(A, 1.0 / 9.0),
+        "neighbours mirrored (k -> 8-k)": A[..., ::-1].copy(),
+        "query and key swapped": oracle.attention(cfg, I, P),
+        "scores from P.P": oracle.attention(cfg, P, P),
+        "scores without 1/sqrt(d)": oracle.attention(cfg, np.sqrt(64.0) * P, I),
+        "value of the centre cell only": centre,
+        "attention map transposed (y <-> x)": A.transpose(0, 2, 1, 3, 4).copy(),
+    }
+    for name, Aw in planted.items():
+        moved = norm_err(y_of(Aw), Y)
+        print(f"  G={G} {name}: Y moves by {moved:.3f}")
+        assert moved > 5 * bar, name
+    rounding = norm_err(round_bf16(y_of(round_bf16(A))), Y)
+    print(f"  G={G} device rounding: {rounding:.2e}")
+    assert rounding < bar / 4
+    # the whole step from unrounded projections stays inside the bar as well
+    assert norm_err(oracle.step(cfg, X, p, 1)[0], Y) < bar / 4
+
+
 # ---- S6 update and mixing ----------------------------------------------------------------
 
 def test_mix_closed_forms(oracle):
