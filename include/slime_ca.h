@@ -49,6 +49,8 @@
 #ifndef SLIME_CA_H
 #define SLIME_CA_H
 
+#include <stddef.h> /* size_t */
+
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -59,6 +61,7 @@ extern "C" {
 #define SLIME_EHIP (-3)    /* HIP runtime error */
 #define SLIME_ENODEV (-4)  /* no usable gfx950 device */
 #define SLIME_ESTATE (-5)  /* call out of order (e.g. step before set_params) */
+#define SLIME_ENONFINITE (-6) /* a conserved sum is NaN or Inf: the state holds one */
 
 #define SLIME_F32 0
 #define SLIME_BF16 1
@@ -74,8 +77,13 @@ typedef struct {
     float dt;            /* update step, 0.1 in the reference (slime/core/organism.cu:659) */
     int growth_per_cell; /* 0: mu, sigma per head; 1: per cell and head */
     int pods;            /* independent parameter sets; B % pods == 0 */
-    int pvi_chain;       /* 0: P, I, V all from X; 1: I from P and V from I
-                            (the chained form of slime/core/pseudopod.cu:98-119) */
+    int pvi_chain;       /* 0: P, I, V all from X;
+                            1: I from P and V from I (the chained form of
+                               slime/core/pseudopod.cu:98-119), P from X;
+                            2: as 1, with P from the toroidal 3x3 neighbourhood sum
+                               of X, the perception of multi_head_ca_kernel
+                               (slime/core/pseudopod.cu:62-91, which clamps at the
+                               border instead of wrapping) */
 } slime_ca_config;
 
 typedef struct {
@@ -92,11 +100,22 @@ typedef struct {
 int slime_ca_create(const slime_ca_config* config, slime_ca** out);
 int slime_ca_destroy(slime_ca* ca);
 
-/* Uploads parameters (host fp32, layouts above). Synchronous. */
+/* Uploads parameters (host fp32, layouts above). Synchronous. Every array is
+ * checked first (slime_ca_check_params): a NaN or Inf entry is SLIME_EINVAL and
+ * leaves the handle's parameters as they were. */
 int slime_ca_set_params(slime_ca* ca, const slime_ca_params* params);
 
-/* S1: P = ReLU(X W_P), I = GELU_tanh(X W_I) (or of P W_I when chained),
- * V = X W_V (or I W_V). P, I, V are [B][G][G][C] in the handle's dtype. */
+/* The host-side checks of slime_ca_set_params for a configuration, without a handle
+ * or a device: the config is valid, no pointer is NULL and every entry of the
+ * arrays (sizes from the config) is finite. SLIME_OK or SLIME_EINVAL. The
+ * reference uploads its parameters unchecked (init_multihead_ca_kernel,
+ * slime/core/pseudopod.cu:386-444). */
+int slime_ca_check_params(const slime_ca_config* config, const slime_ca_params* params);
+
+/* S1: P = ReLU(X W_P) (X replaced by its 3x3 neighbourhood sum for pvi_chain 2),
+ * I = GELU_tanh(X W_I) (or of P W_I when chained), V = X W_V (or I W_V). P, I, V
+ * are [B][G][G][C] in the handle's dtype, distinct from x_in and from each other
+ * (pvi_chain 2 uses V as scratch for the neighbourhood sum before V's product). */
 int slime_ca_project(slime_ca* ca, const void* x_in, void* P, void* I, void* V, void* stream);
 
 /* S2-S7 on given projections: 3x3 toroidal potential, bell growth, 3x3 CA
@@ -110,7 +129,9 @@ int slime_ca_flow_lenia(slime_ca* ca, const void* x_in, const void* P, const voi
 int slime_ca_step(slime_ca* ca, const void* x_in, void* x_out, int n_steps, void* stream);
 
 /* Host copies of the last step's per-(b, head) input mass and output mass
- * (after conservation), B*H doubles each. Synchronises the last stream used. */
+ * (after conservation), B*H doubles each (either pointer may be NULL).
+ * Synchronises the last stream used. SLIME_ENONFINITE, with the copies made, when
+ * a sum is NaN or Inf: the step's input or output held a non-finite value. */
 int slime_ca_mass(slime_ca* ca, double* h_mass_in, double* h_mass_out);
 
 /* E1-E5 over a device history [T][B][G][G][C] (2 <= T <= 65): per (b, head)
@@ -170,9 +191,12 @@ int slime_ca_fitness_scaled(slime_ca* ca, const void* x_hist, const double* scal
  * static device buffer of 32 MiB per GPU that the library holds until the process
  * ends; B*H*chunks*(D*D + 3T) fp64 partials must fit, with the chunk count lowered
  * from slime_ca_fitness's when needed (which can change the last bits of the Gram
- * sums), else SLIME_EINVAL. Every call on a GPU shares that buffer: calls that
- * overlap on one GPU race. The first call on a device looks up the buffer's
- * address there (make it outside graph capture). config gives B, G, H, D and
+ * sums), else SLIME_EINVAL. Every call on a GPU shares that buffer: a call on
+ * another stream than the previous call's waits for it (an event recorded after
+ * each call), but under graph capture no event is used, and replays that overlap
+ * on one GPU race. Loading the library reserves the buffer on every GPU it runs
+ * on. The first call on a device looks up the buffer's address there and creates
+ * its event (make it outside graph capture). config gives B, G, H, D and
  * dtype of the history (its other fields are validated but unused); outputs as
  * slime_ca_fitness; no sweep counts. */
 int slime_ca_fitness_static(const slime_ca_config* config, const void* x_hist, int T,

@@ -43,7 +43,7 @@ class OracleConfig:
     D: int
     pods: int = 1
     growth_per_cell: bool = False
-    pvi_chain: bool = False
+    pvi_chain: int = 0  # 0 parallel, 1 chained, 2 chained with the 3x3 perception sum
     dt: float = 0.1
 
     @property

@@ -6,7 +6,9 @@
 // Reference sources each function follows (paths under the J0pari/Slime tree):
 //   S1 projections   slime/core/pseudopod.cu:29-32 (per-head weight tensors),
 //                    :94 (ReLU), :106-108 (tanh GELU); buildplan.md:572-591
-//                    (P, I, V all from the neighbourhood input)
+//                    (P, I, V all from the neighbourhood input); the chained
+//                    forms of :98-119, with the 3x3 neighbourhood sum of :62-91
+//                    before the perception product in chain mode 2
 //   S2 potential     slime/core/pseudopod.cu:168-180 (per-head 3x3 flow kernel),
 //                    toroidal wrap as slime/kernels/warp_ca.cu:305-310 and
 //                    slime/kernels/triton_impl.cu:90-105
@@ -108,9 +110,37 @@ void project(const Dims& d, const double* in, const float* W, int act, double* o
     }
 }
 
+// The perception input of multi_head_ca_kernel (slime/core/pseudopod.cu:62-91): each
+// channel summed over the 3x3 neighbourhood before the product, the border wrapped
+// (toroidal, as S2) where the reference clamps. Taps in the order k = 3(dy+1)+(dx+1).
+void neighbourhood_sum(const Dims& d, const double* X, double* S) {
+    const int G = d.G, C = d.C;
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int b = 0; b < d.B; ++b)
+        for (int y = 0; y < G; ++y)
+            for (int x = 0; x < G; ++x) {
+                double* s = S + (((size_t)b * G + y) * G + x) * C;
+                for (int ch = 0; ch < C; ++ch) s[ch] = 0.0;
+                for (int dy = -1; dy <= 1; ++dy)
+                    for (int dx = -1; dx <= 1; ++dx) {
+                        const double* xn =
+                            X + (((size_t)b * G + wrap(y + dy, G)) * G + wrap(x + dx, G)) * C;
+                        for (int ch = 0; ch < C; ++ch) s[ch] += xn[ch];
+                    }
+            }
+}
+
+// chain: 0 P, I, V all from X; 1 I from P, V from I; 2 as 1 with P from the
+// neighbourhood sum of X.
 void project_all(const Dims& d, int chain, const double* X, const float* WP, const float* WI,
                  const float* WV, double* P, double* I, double* V) {
-    project(d, X, WP, 1, P);
+    if (chain == 2) {
+        std::vector<double> S((size_t)d.B * d.cells * d.C);
+        neighbourhood_sum(d, X, S.data());
+        project(d, S.data(), WP, 1, P);
+    } else {
+        project(d, X, WP, 1, P);
+    }
     project(d, chain ? P : X, WI, 2, I);
     project(d, chain ? I : X, WV, 0, V);
 }

@@ -29,7 +29,7 @@ typedef struct {
     int B, G, H, D;
     int pods;
     int growth_per_cell;
-    int pvi_chain;
+    int pvi_chain; /* 0 parallel; 1 chained; 2 chained, P from the 3x3 neighbourhood sum */
     float dt;
 } oracle_ca_cfg;
 

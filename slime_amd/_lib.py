@@ -16,6 +16,7 @@ SLIME_ENOMEM = -2
 SLIME_EHIP = -3
 SLIME_ENODEV = -4
 SLIME_ESTATE = -5
+SLIME_ENONFINITE = -6
 SLIME_F32 = 0
 SLIME_BF16 = 1
 
@@ -29,7 +30,7 @@ EXPORTS = (
     "slime_neural_ca_update", "slime_ca_backward", "slime_pool_init", "slime_pool_set_fitness",
     "slime_ca_hunger", "slime_pool_age", "slime_pool_cull", "slime_pool_spawn", "slime_pool_spawn_wave",
     "slime_pool_evolve", "slime_snapshot_json", "slime_ca_fitness_static", "slime_ca_rollout",
-    "slime_ca_fitness_scaled",
+    "slime_ca_fitness_scaled", "slime_ca_check_params",
 )
 
 
@@ -84,6 +85,7 @@ def load() -> ctypes.CDLL:
         "slime_ca_create": [ctypes.POINTER(Config), ctypes.POINTER(ctypes.c_void_p)],
         "slime_ca_destroy": [vp],
         "slime_ca_set_params": [vp, ctypes.POINTER(Params)],
+        "slime_ca_check_params": [ctypes.POINTER(Config), ctypes.POINTER(Params)],
         "slime_ca_project": [vp, vp, vp, vp, vp, vp],
         "slime_ca_flow_lenia": [vp, vp, vp, vp, vp, vp, vp],
         "slime_ca_step": [vp, vp, vp, i, vp],

@@ -35,11 +35,16 @@ def _stream(stream=None) -> ctypes.c_void_p:
 
 
 class Pseudopod:
-    """One multi-head neural-CA engine (a ``slime_ca`` handle)."""
+    """One multi-head neural-CA engine (a ``slime_ca`` handle).
+
+    ``pvi_chain``: 0 computes P, I and V from the state; 1 chains them (I from P,
+    V from I, slime/core/pseudopod.cu:98-119); 2 chains them with P from the 3x3
+    neighbourhood sum of the state, the perception of multi_head_ca_kernel
+    (slime/core/pseudopod.cu:62-91, toroidal here)."""
 
     def __init__(self, B: int, G: int, H: int = 8, D: int = 64, dtype: str = "bf16",
                  dt: float = 0.1, growth_per_cell: bool = False, pods: int = 1,
-                 pvi_chain: bool = False):
+                 pvi_chain: int = 0):
         if dtype not in _DTYPES:
             raise ValueError(f"dtype must be one of {sorted(_DTYPES)}")
         self.lib = _lib.load()

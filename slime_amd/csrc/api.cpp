@@ -139,7 +139,7 @@ int validate(const slime_ca_config* c) {
     if (!std::isfinite(c->dt)) return fail(SLIME_EINVAL, "dt is not finite");
     if (c->growth_per_cell != 0 && c->growth_per_cell != 1)
         return fail(SLIME_EINVAL, "growth_per_cell must be 0 or 1");
-    if (c->pvi_chain != 0 && c->pvi_chain != 1) return fail(SLIME_EINVAL, "pvi_chain must be 0 or 1");
+    if (c->pvi_chain < 0 || c->pvi_chain > 2) return fail(SLIME_EINVAL, "pvi_chain must be 0, 1 or 2");
     const double elems = (double)c->B * c->G * c->G * c->H * c->D;
     if (elems > 4.0e9) return fail(SLIME_EINVAL, "state of %.3g elements is too large", elems);
     // The stencils address one batch entry with 32-bit offsets: element offsets in
@@ -196,11 +196,30 @@ size_t n_param_growth(const slime_ca_config& c) {
     return c.growth_per_cell ? (size_t)c.pods * c.G * c.G * c.H : (size_t)c.pods * c.H;
 }
 
-int use_handle(slime_ca* h) {
-    if (!h) return fail(SLIME_EINVAL, "handle is NULL");
-    HIP_TRY(hipSetDevice(h->device));
-    return SLIME_OK;
-}
+// Makes the handle's device current for the rest of an entry point and gives the
+// caller's current device back when the entry point returns.
+class DeviceScope {
+  public:
+    DeviceScope() = default;
+    DeviceScope(const DeviceScope&) = delete;
+    DeviceScope& operator=(const DeviceScope&) = delete;
+    ~DeviceScope() {
+        if (restore_) (void)hipSetDevice(prev_);
+    }
+    int enter(const slime_ca* h) {
+        if (!h) return fail(SLIME_EINVAL, "handle is NULL");
+        if (hipGetDevice(&prev_) != hipSuccess) prev_ = -1;
+        if (prev_ != h->device) {
+            HIP_TRY(hipSetDevice(h->device));
+            restore_ = prev_ >= 0;
+        }
+        return SLIME_OK;
+    }
+
+  private:
+    int prev_ = -1;
+    bool restore_ = false;
+};
 
 // S1 for one step: per-batch weights (scaled by the deferred mass scale of x),
 // then the projection GEMM(s).
@@ -238,7 +257,12 @@ int run_project(slime_ca* h, const void* x, const float* x_scale, void* P, void*
         g.act[2] = 0;
         HIP_TRY(timed(h, h->gemm_ev, s, [&] { return launch_gemm(c.dtype, g, s); }));
     } else {
-        const void* ins[3] = {x, P, I};
+        // pvi_chain 2: P reads the 3x3 neighbourhood sum of x, held in V until V's own
+        // product overwrites it. The deferred mass scale of x is per (b, head), so it
+        // scales the neighbourhood sum as it scales x, and plane 0 still carries it.
+        if (c.pvi_chain == 2)
+            HIP_TRY(launch_neighbourhood_sum(c.dtype, x, V, c.B, c.G, C, s));
+        const void* ins[3] = {c.pvi_chain == 2 ? static_cast<const void*>(V) : x, P, I};
         void* outs[3] = {P, I, V};
         const int acts[3] = {1, 2, 0};
         g.N = C;
@@ -412,26 +436,48 @@ int slime_ca_create(const slime_ca_config* config, slime_ca** out) {
 
 int slime_ca_destroy(slime_ca* h) {
     if (!h) return SLIME_OK;
-    (void)hipSetDevice(h->device);
+    DeviceScope scope;
+    (void)scope.enter(h);
     (void)hipDeviceSynchronize();
     release(h);
     delete h;
     return SLIME_OK;
 }
 
-int slime_ca_set_params(slime_ca* h, const slime_ca_params* p) {
-    int rc = use_handle(h);
+int slime_ca_check_params(const slime_ca_config* config, const slime_ca_params* p) {
+    int rc = validate(config);
     if (rc) return rc;
     if (!p || !p->WP || !p->WI || !p->WV || !p->K || !p->mu || !p->sigma || !p->M)
         return fail(SLIME_EINVAL, "a parameter pointer is NULL");
+    const slime_ca_config& c = *config;
+    const size_t C = (size_t)c.H * c.D, CC = C * C;
+    const size_t ng = n_param_growth(c);
+    const struct {
+        const char* name;
+        const float* v;
+        size_t n;
+    } arrays[] = {{"WP", p->WP, (size_t)c.pods * CC}, {"WI", p->WI, (size_t)c.pods * CC},
+                  {"WV", p->WV, (size_t)c.pods * CC}, {"K", p->K, (size_t)c.pods * c.H * 9},
+                  {"M", p->M, (size_t)c.pods * c.H * c.H}, {"mu", p->mu, ng},
+                  {"sigma", p->sigma, ng}};
+    for (const auto& a : arrays)
+        for (size_t i = 0; i < a.n; ++i)
+            if (!std::isfinite(a.v[i]))
+                return fail(SLIME_EINVAL, "%s entry %zu is not finite", a.name, i);
+    return SLIME_OK;
+}
+
+int slime_ca_set_params(slime_ca* h, const slime_ca_params* p) {
+    DeviceScope scope;
+    int rc = scope.enter(h);
+    if (rc) return rc;
     const slime_ca_config& c = h->cfg;
     const size_t C = h->C, CC = C * C;
+    const size_t ng = n_param_growth(c);
     // Every input is checked before the first upload, so a rejected call leaves the
     // handle's parameters as they were.
-    const size_t ng = n_param_growth(c);
-    for (size_t i = 0; i < ng; ++i)
-        if (!std::isfinite(p->sigma[i]) || !std::isfinite(p->mu[i]))
-            return fail(SLIME_EINVAL, "mu/sigma entry %zu is not finite", i);
+    rc = slime_ca_check_params(&c, p);
+    if (rc) return rc;
     // From here a failed upload leaves a mix of old and new parameters: the handle
     // refuses to step until a later call succeeds.
     h->params_set = false;
@@ -476,10 +522,13 @@ int slime_ca_set_params(slime_ca* h, const slime_ca_params* p) {
 }
 
 int slime_ca_project(slime_ca* h, const void* x_in, void* P, void* I, void* V, void* stream) {
-    int rc = use_handle(h);
+    DeviceScope scope;
+    int rc = scope.enter(h);
     if (rc) return rc;
     if (!h->params_set) return fail(SLIME_ESTATE, "slime_ca_set_params has not been called");
     if (!x_in || !P || !I || !V) return fail(SLIME_EINVAL, "a tensor pointer is NULL");
+    if (P == x_in || I == x_in || V == x_in || P == I || P == V || I == V)
+        return fail(SLIME_EINVAL, "P, I and V must be distinct from x_in and from each other");
     hipStream_t s = static_cast<hipStream_t>(stream);
     h->last_stream = s;
     return run_project(h, x_in, nullptr, P, I, V, s);
@@ -487,7 +536,8 @@ int slime_ca_project(slime_ca* h, const void* x_in, void* P, void* I, void* V, v
 
 int slime_ca_flow_lenia(slime_ca* h, const void* x_in, const void* P, const void* I, const void* V,
                         void* y_out, void* stream) {
-    int rc = use_handle(h);
+    DeviceScope scope;
+    int rc = scope.enter(h);
     if (rc) return rc;
     if (!h->params_set) return fail(SLIME_ESTATE, "slime_ca_set_params has not been called");
     if (!x_in || !P || !I || !V || !y_out) return fail(SLIME_EINVAL, "a tensor pointer is NULL");
@@ -506,7 +556,8 @@ int slime_ca_flow_lenia(slime_ca* h, const void* x_in, const void* P, const void
 }
 
 int slime_ca_step(slime_ca* h, const void* x_in, void* x_out, int n_steps, void* stream) {
-    int rc = use_handle(h);
+    DeviceScope scope;
+    int rc = scope.enter(h);
     if (rc) return rc;
     if (!h->params_set) return fail(SLIME_ESTATE, "slime_ca_set_params has not been called");
     if (!x_in || !x_out) return fail(SLIME_EINVAL, "a tensor pointer is NULL");
@@ -544,19 +595,33 @@ int slime_ca_step(slime_ca* h, const void* x_in, void* x_out, int n_steps, void*
 }
 
 int slime_ca_mass(slime_ca* h, double* h_in, double* h_out) {
-    int rc = use_handle(h);
+    DeviceScope scope;
+    int rc = scope.enter(h);
     if (rc) return rc;
     if (!h_in && !h_out) return fail(SLIME_EINVAL, "both outputs are NULL");
     const size_t BH = (size_t)h->cfg.B * h->cfg.H;
     HIP_TRY(hipStreamSynchronize(h->last_stream));
-    if (h_in) HIP_TRY(hipMemcpy(h_in, h->mass_in, BH * 8, hipMemcpyDeviceToHost));
-    if (h_out) HIP_TRY(hipMemcpy(h_out, h->mass_out, BH * 8, hipMemcpyDeviceToHost));
+    std::vector<double> in(BH), out(BH);
+    HIP_TRY(hipMemcpy(in.data(), h->mass_in, BH * 8, hipMemcpyDeviceToHost));
+    HIP_TRY(hipMemcpy(out.data(), h->mass_out, BH * 8, hipMemcpyDeviceToHost));
+    if (h_in) std::memcpy(h_in, in.data(), BH * 8);
+    if (h_out) std::memcpy(h_out, out.data(), BH * 8);
+    // A NaN or Inf anywhere in a (batch, head) block reaches its fp64 sums, so they
+    // report a non-finite state (the reference detects and reports failures, CUDA_CHECK
+    // at slime/runtime.cu:11-20; here with a status code).
+    for (size_t i = 0; i < BH; ++i)
+        if (!std::isfinite(in[i]) || !std::isfinite(out[i]))
+            return fail(SLIME_ENONFINITE,
+                        "mass of batch %zu head %zu is not finite (in %g, out %g): the state "
+                        "holds NaN or Inf",
+                        i / h->cfg.H, i % h->cfg.H, in[i], out[i]);
     return SLIME_OK;
 }
 
 int slime_ca_fitness(slime_ca* h, const void* x_hist, int T, float* erank, float* coherence,
                      float* fitness, void* stream) {
-    int rc = use_handle(h);
+    DeviceScope scope;
+    int rc = scope.enter(h);
     if (rc) return rc;
     if (!x_hist || !erank || !coherence || !fitness)
         return fail(SLIME_EINVAL, "a tensor pointer is NULL");
@@ -566,7 +631,8 @@ int slime_ca_fitness(slime_ca* h, const void* x_hist, int T, float* erank, float
 }
 
 int slime_ca_rollout(slime_ca* h, void* hist, int T, double* scales, void* stream) {
-    int rc = use_handle(h);
+    DeviceScope scope;
+    int rc = scope.enter(h);
     if (rc) return rc;
     if (!h->params_set) return fail(SLIME_ESTATE, "slime_ca_set_params has not been called");
     if (!hist || !scales) return fail(SLIME_EINVAL, "a tensor pointer is NULL");
@@ -597,7 +663,8 @@ int slime_ca_rollout(slime_ca* h, void* hist, int T, double* scales, void* strea
 
 int slime_ca_fitness_scaled(slime_ca* h, const void* x_hist, const double* scales, int T,
                             float* erank, float* coherence, float* fitness, void* stream) {
-    int rc = use_handle(h);
+    DeviceScope scope;
+    int rc = scope.enter(h);
     if (rc) return rc;
     if (!x_hist || !scales || !erank || !coherence || !fitness)
         return fail(SLIME_EINVAL, "a tensor pointer is NULL");
@@ -624,10 +691,6 @@ int slime_ca_fitness_static(const slime_ca_config* config, const void* x_hist, i
     int ndev = 0;
     if (hipGetDeviceCount(&ndev) != hipSuccess || ndev < 1)
         return fail(SLIME_ENODEV, "no HIP device visible");
-    void* scr = nullptr;
-    const hipError_t e = fitness_static_scratch(&scr);
-    if (e == hipErrorNoBinaryForGpu) return fail(SLIME_ENODEV, "the current device is not a gfx950");
-    HIP_TRY(e);
     FitnessArgs f{};
     f.hist = x_hist;
     f.t_stride = (long long)c.B * c.G * c.G * c.H * c.D * (c.dtype == SLIME_BF16 ? 2 : 4);
@@ -636,18 +699,19 @@ int slime_ca_fitness_static(const slime_ca_config* config, const void* x_hist, i
     f.G = c.G;
     f.D = c.D;
     f.chunks = chunks;
-    f.gram_part = static_cast<double*>(scr);
-    f.mom_part = f.gram_part + (size_t)c.B * c.H * chunks * c.D * c.D;
     f.erank = erank;
     f.coh = coherence;
     f.fitness = fitness;
     f.sweeps = nullptr;
-    HIP_TRY(launch_fitness(c.dtype, f, static_cast<hipStream_t>(stream)));
+    const hipError_t e = launch_fitness_static(c.dtype, f, static_cast<hipStream_t>(stream));
+    if (e == hipErrorNoBinaryForGpu) return fail(SLIME_ENODEV, "the current device is not a gfx950");
+    HIP_TRY(e);
     return SLIME_OK;
 }
 
 int slime_ca_fitness_sweeps(slime_ca* h, int* h_sweeps) {
-    int rc = use_handle(h);
+    DeviceScope scope;
+    int rc = scope.enter(h);
     if (rc) return rc;
     if (!h_sweeps) return fail(SLIME_EINVAL, "output is NULL");
     HIP_TRY(hipStreamSynchronize(h->last_stream));
@@ -657,7 +721,8 @@ int slime_ca_fitness_sweeps(slime_ca* h, int* h_sweeps) {
 }
 
 int slime_ca_init_from_field(slime_ca* h, const float* conc, void* x, void* stream) {
-    int rc = use_handle(h);
+    DeviceScope scope;
+    int rc = scope.enter(h);
     if (rc) return rc;
     if (!conc || !x) return fail(SLIME_EINVAL, "a tensor pointer is NULL");
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -667,7 +732,8 @@ int slime_ca_init_from_field(slime_ca* h, const float* conc, void* x, void* stre
 }
 
 int slime_ca_field_from_state(slime_ca* h, const void* x, float* conc, void* stream) {
-    int rc = use_handle(h);
+    DeviceScope scope;
+    int rc = scope.enter(h);
     if (rc) return rc;
     if (!conc || !x) return fail(SLIME_EINVAL, "a tensor pointer is NULL");
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -677,7 +743,8 @@ int slime_ca_field_from_state(slime_ca* h, const void* x, float* conc, void* str
 }
 
 int slime_ca_get_state(slime_ca* h, const void* x, float* h_buffer, int size) {
-    int rc = use_handle(h);
+    DeviceScope scope;
+    int rc = scope.enter(h);
     if (rc) return rc;
     if (!x || !h_buffer) return fail(SLIME_EINVAL, "a pointer is NULL");
     const long long cells = (long long)h->cfg.G * h->cfg.G;
@@ -696,7 +763,8 @@ int slime_ca_get_state(slime_ca* h, const void* x, float* h_buffer, int size) {
 
 int slime_neural_ca_update(slime_ca* h, const slime_multihead_ca_state* st, float* conc,
                            float* erank_hist, int generation, void* stream) {
-    int rc = use_handle(h);
+    DeviceScope scope;
+    int rc = scope.enter(h);
     if (rc) return rc;
     if (!h->params_set) return fail(SLIME_ESTATE, "slime_ca_set_params has not been called");
     if (!st || !st->ca_input || !st->ca_output || !conc || !erank_hist)
@@ -730,7 +798,8 @@ int slime_neural_ca_update(slime_ca* h, const slime_multihead_ca_state* st, floa
 
 int slime_ca_backward(slime_ca* h, const void* x_in, const void* target, float* grad_x,
                       const slime_ca_grads* grads, double* loss, void* stream) {
-    int rc = use_handle(h);
+    DeviceScope scope;
+    int rc = scope.enter(h);
     if (rc) return rc;
     if (!h->params_set) return fail(SLIME_ESTATE, "slime_ca_set_params has not been called");
     if (!x_in || !target || !grad_x) return fail(SLIME_EINVAL, "a tensor pointer is NULL");
@@ -763,7 +832,7 @@ int slime_ca_backward(slime_ca* h, const void* x_in, const void* target, float* 
     rc = 0;
     if (!h->Ipre) rc = rc ? rc : dalloc(&h->Ipre, n * h->elem);
     if (!h->bw_lpart) rc = rc ? rc : dalloc_t(&h->bw_lpart, BH * lchunks * 3 * 8);
-    if (!h->bw_coef) rc = rc ? rc : dalloc_t(&h->bw_coef, BH * 2 * 4);
+    if (!h->bw_coef) rc = rc ? rc : dalloc_t(&h->bw_coef, BH * 3 * 4);
     if (!h->bw_loss) rc = rc ? rc : dalloc_t(&h->bw_loss, BH * 8);
     if (!h->bw_gU) rc = rc ? rc : dalloc_t(&h->bw_gU, n * 4);
     if (!h->bw_gVt) rc = rc ? rc : dalloc_t(&h->bw_gVt, n * 4);
@@ -892,7 +961,8 @@ int slime_ca_backward(slime_ca* h, const void* x_in, const void* target, float* 
 }
 
 int slime_ca_set_timing(slime_ca* h, int enable) {
-    int rc = use_handle(h);
+    DeviceScope scope;
+    int rc = scope.enter(h);
     if (rc) return rc;
     if (h->last_stream || h->ev_used) HIP_TRY(hipStreamSynchronize(h->last_stream));
     h->timing = enable != 0;
@@ -903,7 +973,8 @@ int slime_ca_set_timing(slime_ca* h, int enable) {
 }
 
 int slime_ca_timings(slime_ca* h, double* gemm_ms, int* gemm_n, double* stencil_ms, int* stencil_n) {
-    int rc = use_handle(h);
+    DeviceScope scope;
+    int rc = scope.enter(h);
     if (rc) return rc;
     HIP_TRY(hipStreamSynchronize(h->last_stream));
     auto sum = [&](const std::vector<std::pair<size_t, size_t>>& log, double* ms, int* n) -> int {
@@ -1016,7 +1087,8 @@ int slime_snapshot_json(const slime_ca* h, const float* conc, const slime_pool* 
     if (!h->params_set) return fail(SLIME_ESTATE, "parameters not set");
     if (!std::isfinite(elapsed)) return fail(SLIME_EINVAL, "elapsed is not finite");
     const slime_ca_config& c = h->cfg;
-    HIP_TRY(hipSetDevice(h->device));
+    DeviceScope scope;
+    if (int rc = scope.enter(h)) return rc;
     const int n = c.G < 16 ? c.G : 16, off = (c.G - n) / 2;
     std::vector<float> sample((size_t)n * n), K((size_t)c.H * 9);
     HIP_TRY(hipMemcpy2D(sample.data(), n * sizeof(float), conc + (size_t)off * c.G + off,

@@ -138,7 +138,8 @@ __global__ __launch_bounds__(256) void bw_loss_partial_kernel(BackwardArgs a) {
     const int h = 4 * t / a.D;
     const long long cells = (long long)a.G * a.G;
     const double N = (double)a.B * (double)cells * C;
-    const float r = a.scale[b * kHeads + h];
+    const int BH = a.B * kHeads;
+    const double r = (double)a.scale[b * kHeads + h] + (double)a.scale[BH + b * kHeads + h];
     double l = 0.0, q = 0.0, bs = 0.0;
     if (slot < slots) {
         for (int c0 = slot; c0 < kLossCells; c0 += slots) {
@@ -149,7 +150,7 @@ __global__ __launch_bounds__(256) void bw_loss_partial_kernel(BackwardArgs a) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const double yd = y.v[e];
-                const double err = (double)r * yd - (double)tv.v[e];
+                const double err = r * yd - (double)tv.v[e];
                 l += err * err;
                 q += err * yd;
                 bs += yd;
@@ -198,8 +199,9 @@ __global__ __launch_bounds__(256) void bw_loss_finalize_kernel(BackwardArgs a) {
     if (threadIdx.x == 0) {
         const double ls = s[0][0], qs = s[1][0], b_s = s[2][0];
         const bool guard = fabs(b_s) > 1e-6;
-        a.coef[bh * 2 + 0] = guard ? a.scale[bh] : 1.0f;
-        a.coef[bh * 2 + 1] = guard ? (float)(qs / b_s) : 0.0f;
+        a.coef[bh * 3 + 0] = guard ? a.scale[bh] : 1.0f;
+        a.coef[bh * 3 + 1] = guard ? (float)(qs / b_s) : 0.0f;
+        a.coef[bh * 3 + 2] = guard ? a.scale[gridDim.x + bh] : 0.0f;
         a.loss_bh[bh] = ls;
     }
 }
@@ -349,11 +351,17 @@ void bw_cell_kernel(BackwardArgs a) {
         for (int e = 0; e < 4; ++e) z[e] = __builtin_fmaf(dt * g[e], vt[e], raw_at<T>(xk[4], e));
         // ---- S7 -> gY of output head h at (r, c0..c0+3), shared; S6 -> gZ_h ----
         {
-            const float rs = a.scale[b * H + h];
-            const float cy = a.coef[(b * H + h) * 2], cq = a.coef[(b * H + h) * 2 + 1];
+            const float rs = a.scale[b * H + h], rsl = a.scale[a.B * H + b * H + h];
+            const float* cf = a.coef + (b * H + h) * 3;
+            const float cy = cf[0], cq = cf[1], cyl = cf[2];
             float gyo[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) gyo[e] = cy * (2.0f * (rs * yv.v[e] - tv.v[e]) * a.inv_n - cq);
+            for (int e = 0; e < 4; ++e) {
+                // y = (hi + lo) raw and gY = (cy_hi + cy_lo) u, each as an fma of the
+                // high part over the product of the low part, as the forward scales
+                const float u = 2.0f * (__builtin_fmaf(rs, yv.v[e], rsl * yv.v[e]) - tv.v[e]) * a.inv_n - cq;
+                gyo[e] = __builtin_fmaf(cy, u, cyl * u);
+            }
             *reinterpret_cast<float4*>(sgy + cs * C + h * kD + c0) = make_float4(gyo[0], gyo[1], gyo[2], gyo[3]);
         }
         __syncthreads();
@@ -438,7 +446,7 @@ void bw_cell_kernel(BackwardArgs a) {
         st4f(a.gVt, ir, gvt);
         // gP~ -> plane 0 of G3; the direct part of gX
         float gpt[4], gxd[4];
-        const float cqh = a.coef[(b * H + h) * 2 + 1];
+        const float cqh = a.coef[(b * H + h) * 3 + 1];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             gpt[e] = pc.v[e] > 0.f ? gp[e] : 0.f;

@@ -28,10 +28,12 @@
 
 // Scratch of the allocation-free entry point slime_ca_fitness_static: the Gram and
 // moment partials of one call. One copy per GPU, created when the code object loads
-// on that device and held until the process ends; every call on a GPU shares it, so
-// calls that overlap on one GPU race. Host code never takes the array's name as an
-// address (on the host it is only a stand-in for the symbol): fitness_static_scratch
-// looks the device address up once per device and kernels receive that pointer.
+// on that device and held until the process ends; every call on a GPU shares it.
+// Calls on different streams are ordered by launch_fitness_static (each waits for the
+// previous call's event); calls under graph capture are not, and replays that overlap
+// on one GPU race. Host code never takes the array's name as an address (on the host
+// it is only a stand-in for the symbol): the device address is looked up once per
+// device and kernels receive that pointer.
 static __device__ __align__(256) unsigned char scratch[slime::kFitnessScratchBytes];
 
 namespace slime {
@@ -468,16 +470,26 @@ int fitness_static_chunks(int B, int G, int D, int T) {
     return 0;
 }
 
-hipError_t fitness_static_scratch(void** ptr) {
-    constexpr int kMaxDevices = 64;
-    static std::mutex mu;
-    static void* addr[kMaxDevices] = {};
+namespace {
+// Per device: the scratch's device address, and the event and stream of the last
+// call that launched outside graph capture.
+struct StaticSlot {
+    void* addr = nullptr;
+    hipEvent_t done = nullptr;
+    hipStream_t last = nullptr;
+    bool recorded = false;
+};
+constexpr int kMaxDevices = 64;
+std::mutex g_static_mu;
+StaticSlot g_static[kMaxDevices];
+
+hipError_t static_slot(StaticSlot** out) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
     if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
-    std::lock_guard<std::mutex> lock(mu);
-    if (!addr[dev]) {
+    StaticSlot& s = g_static[dev];
+    if (!s.addr) {
         hipDeviceProp_t prop;
         e = hipGetDeviceProperties(&prop, dev);
         if (e != hipSuccess) return e;
@@ -486,10 +498,48 @@ hipError_t fitness_static_scratch(void** ptr) {
         e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
         if (e != hipSuccess) return e;
         if (!p) return hipErrorInvalidSymbol;
-        addr[dev] = p;
+        e = hipEventCreateWithFlags(&s.done, hipEventDisableTiming);
+        if (e != hipSuccess) return e;
+        s.addr = p;
     }
-    *ptr = addr[dev];
+    *out = &s;
     return hipSuccess;
+}
+}  // namespace
+
+hipError_t fitness_static_scratch(void** ptr) {
+    std::lock_guard<std::mutex> lock(g_static_mu);
+    StaticSlot* s = nullptr;
+    const hipError_t e = static_slot(&s);
+    if (e == hipSuccess) *ptr = s->addr;
+    return e;
+}
+
+hipError_t launch_fitness_static(int dtype, FitnessArgs f, hipStream_t stream) {
+    std::lock_guard<std::mutex> lock(g_static_mu);
+    StaticSlot* s = nullptr;
+    hipError_t e = static_slot(&s);
+    if (e != hipSuccess) return e;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(stream, &cap);
+    if (e != hipSuccess) return e;
+    const bool ordered = cap == hipStreamCaptureStatusNone;
+    // The previous call's kernels, if they ran on another stream, finish with the
+    // scratch before this call's kernels write it.
+    if (ordered && s->recorded && s->last != stream) {
+        e = hipStreamWaitEvent(stream, s->done, 0);
+        if (e != hipSuccess) return e;
+    }
+    f.gram_part = static_cast<double*>(s->addr);
+    f.mom_part = f.gram_part + (size_t)f.B * kHeads * f.chunks * f.D * f.D;
+    e = launch_fitness(dtype, f, stream);
+    if (e != hipSuccess || !ordered) return e;
+    e = hipEventRecord(s->done, stream);
+    if (e == hipSuccess) {
+        s->last = stream;
+        s->recorded = true;
+    }
+    return e;
 }
 
 }  // namespace slime

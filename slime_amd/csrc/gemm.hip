@@ -105,19 +105,75 @@ __global__ __launch_bounds__(256) void weight_prep_kernel(WeightPrepArgs w) {
 #pragma unroll 4
     for (int bb = b0; bb < b1; ++bb) {
         const int b = pod * w.per_pod + bb;
+        // scale = hi + lo, applied as w * hi + w * lo with one rounding (the stencil
+        // applies the same factor to its reads of the state)
         const float s = scaled ? w.scale[b * heads + head] : 1.0f;
+        const float sl = scaled ? w.scale[(long long)w.B * heads + b * heads + head] : 0.0f;
+        float o[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = __builtin_fmaf(o[e], s, o[e] * sl);
         if constexpr (sizeof(T) == 2) {
             *reinterpret_cast<uint4*>(static_cast<T*>(w.Wt) + (long long)b * per_b + r) =
-                make_uint4(pack_bf16x2(v0.x * s, v0.y * s), pack_bf16x2(v0.z * s, v0.w * s),
-                           pack_bf16x2(v1.x * s, v1.y * s), pack_bf16x2(v1.z * s, v1.w * s));
+                make_uint4(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]), pack_bf16x2(o[4], o[5]),
+                           pack_bf16x2(o[6], o[7]));
         } else {
             float* dst = static_cast<float*>(w.Wt) + (long long)b * per_b + r;
-            *reinterpret_cast<float4*>(dst) = make_float4(v0.x * s, v0.y * s, v0.z * s, v0.w * s);
-            *reinterpret_cast<float4*>(dst + 4) = make_float4(v1.x * s, v1.y * s, v1.z * s, v1.w * s);
+            *reinterpret_cast<float4*>(dst) = make_float4(o[0], o[1], o[2], o[3]);
+            *reinterpret_cast<float4*>(dst + 4) = make_float4(o[4], o[5], o[6], o[7]);
         }
     }
 }
 }  // namespace
+
+// ---- the reference's perception input: the 3x3 neighbourhood sum -------------------
+namespace {
+// S[b][y][x][c] = sum over the 9 toroidal neighbours (y+dy, x+dx) of X[b][..][..][c],
+// taps in the order k = 3(dy+1)+(dx+1), fp32 sums rounded once to the storage type.
+// One thread per 8 consecutive channels of a cell: a wave reads whole 1 KiB (bf16)
+// or 2 KiB (fp32) cell rows of each neighbour, and the 8 neighbours shared with the
+// adjacent cells come from L2.
+template <typename T>
+__global__ __launch_bounds__(256) void neighbourhood_sum_kernel(const T* X, T* S, int B, int G, int C) {
+    const int groups = C / 8;
+    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (long long)B * G * G * groups) return;
+    const long long cell = idx / groups;
+    const int c0 = (int)(idx - cell * groups) * 8;
+    const long long b = cell / ((long long)G * G);
+    const int yx = (int)(cell - b * G * G);
+    const int y = yx / G, x = yx - y * G;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int dy = -1; dy <= 1; ++dy) {
+        const int yy = y + dy < 0 ? G - 1 : (y + dy == G ? 0 : y + dy);
+        for (int dx = -1; dx <= 1; ++dx) {
+            const int xx = x + dx < 0 ? G - 1 : (x + dx == G ? 0 : x + dx);
+            const T* p = X + ((b * G + yy) * G + xx) * C + c0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float2 v = Store<T>::load2(p + 2 * j);
+                acc[2 * j] += v.x;
+                acc[2 * j + 1] += v.y;
+            }
+        }
+    }
+    T* o = S + cell * C + c0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) Store<T>::store2(o + 2 * j, acc[2 * j], acc[2 * j + 1]);
+}
+}  // namespace
+
+hipError_t launch_neighbourhood_sum(int dtype, const void* X, void* S, int B, int G, int C,
+                                    hipStream_t s) {
+    const long long total = (long long)B * G * G * (C / 8);
+    const dim3 grid((unsigned)((total + 255) / 256));
+    if (dtype == 1)
+        hipLaunchKernelGGL(neighbourhood_sum_kernel<bf16_t>, grid, dim3(256), 0, s,
+                           static_cast<const bf16_t*>(X), static_cast<bf16_t*>(S), B, G, C);
+    else
+        hipLaunchKernelGGL(neighbourhood_sum_kernel<float>, grid, dim3(256), 0, s,
+                           static_cast<const float*>(X), static_cast<float*>(S), B, G, C);
+    return hipGetLastError();
+}
 
 hipError_t launch_weight_prep(int dtype, const WeightPrepArgs& a, hipStream_t s) {
     const long long units = (long long)(a.B / a.per_pod) * a.nplanes * a.C * a.C / 8;

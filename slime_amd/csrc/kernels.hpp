@@ -32,12 +32,19 @@ hipError_t launch_gemm(int dtype, const GemmArgs& a, hipStream_t s);
 // out[0]'s layout (in place allowed); MFMA shapes only (else hipErrorInvalidValue).
 hipError_t launch_gemm_add_f32(int dtype, const GemmArgs& a, const float* add, hipStream_t s);
 
+// The perception input of the reference's S1 (pvi_chain = 2): S = the toroidal 3x3
+// neighbourhood sum of every channel of X, [B][G][G][C] in the storage type
+// (multi_head_ca_kernel sums the neighbourhood before the product,
+// slime/core/pseudopod.cu:62-91). S must not alias X.
+hipError_t launch_neighbourhood_sum(int dtype, const void* X, void* S, int B, int G, int C,
+                                    hipStream_t s);
+
 // ---- per-batch scaled, transposed weights -------------------------------------
 // Wt[b][p*C + n][k] = cvt( scale_p(b, k) * Wtm[pod(b)][p*C + n][k] ), where the
 // mass scale applies only to planes that consume the state (scale[b][k / D]).
 struct WeightPrepArgs {
     const float* Wtm;     // [pods][nplanes*C][C] fp32 masters, already transposed
-    const float* scale;   // [B][H] or nullptr
+    const float* scale;   // [2][B][H] high then low parts (scale = hi + lo), or nullptr
     void* Wt;             // [B][nplanes*C][C]
     int B, C, D, per_pod, nplanes;
     unsigned scaled_planes;  // bit p set: plane p is multiplied by the scale
@@ -123,6 +130,12 @@ constexpr size_t kFitnessScratchBytes = size_t(32) << 20;
 size_t fitness_partial_bytes(int B, int D, int T, int chunks);
 int fitness_static_chunks(int B, int G, int D, int T);
 hipError_t fitness_static_scratch(void** ptr);
+// launch_fitness on the static scratch (f.gram_part and f.mom_part are set here).
+// Outside graph capture, a call on another stream than the previous call's waits for
+// that call's kernels (a per-device event recorded after each launch), so calls from
+// several streams do not overwrite each other's partials; under capture the caller
+// orders its replays.
+hipError_t launch_fitness_static(int dtype, FitnessArgs f, hipStream_t s);
 
 // ---- backward of one step under the MSE loss (backward.hip) --------------------------------
 struct BackwardArgs {
@@ -134,7 +147,7 @@ struct BackwardArgs {
     const void* Ipre;        // I before the GELU (storage type)
     const float* Y;          // [B][G][G][C] unscaled step output, fp32
     const void* T;           // target (storage type)
-    const float* scale;      // [B*H] conservation scale r
+    const float* scale;      // [2][B*H] conservation scale r = hi + lo (high, then low parts)
     const float* K;          // parameters, layouts as StencilArgs
     const float* mu;
     const float* sigma;
@@ -145,7 +158,8 @@ struct BackwardArgs {
     // work buffers
     double* lpart;           // [B*H][lchunks][3]
     int lchunks;             // backward_loss_chunks(G)
-    float* coef;             // [B*H][2]: gY = coef0 (gY' - coef1); coef1 also enters gX
+    float* coef;             // [B*H][3]: gY = (coef0 + coef2) (gY' - coef1), coef0 + coef2 the
+                             // scale r (or 1 under the guard); coef1 also enters gX
     double* loss_bh;         // [B*H] sum of squared errors
     float* gU;               // [B][G][G][C] fp32
     float* gVt;              // [B][G][G][C] fp32

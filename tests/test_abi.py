@@ -113,3 +113,67 @@ def test_probe_library_exports_the_ceiling_probes():
     assert hasattr(lib, "slime_probe_fp64_core")
     ca = _lib.load()
     assert not hasattr(ca, "slime_probe_mfma_tflops")
+
+
+# ---- the header and a compiled host, as a C or C++ caller uses them ---------------------
+
+@pytest.mark.parametrize("lang", ["c", "c++"])
+def test_header_compiles_alone(lang):
+    """include/slime_ca.h alone, as C99 and as C++17, with -Wall -Wextra -Werror
+    -pedantic: it includes what it uses (size_t) and nothing else is assumed."""
+    from tests import binding
+    binding.compile_header(lang)
+
+
+def test_compiled_cpp_host_checks_without_a_gpu():
+    """tests/ca_binding.cpp built with g++ against the header and linked to the
+    library: its status-code checks (EINVAL for bad configurations and non-finite
+    parameters, ENODEV or EHIP for a valid one here) all pass."""
+    import subprocess
+    from tests import binding
+    exe = binding.build_binding()
+    r = subprocess.run([exe, "checks"], capture_output=True, text=True, timeout=60)
+    print(r.stdout)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert r.stdout.strip().endswith("checks ok")
+
+
+def _param_arrays(cfg, fill=0.01):
+    import numpy as np
+    C = cfg.H * cfg.D
+    g = (cfg.pods, cfg.G, cfg.G, cfg.H) if cfg.growth_per_cell else (cfg.pods, cfg.H)
+    return {"WP": np.full((cfg.pods, C, C), fill, np.float32),
+            "WI": np.full((cfg.pods, C, C), fill, np.float32),
+            "WV": np.full((cfg.pods, C, C), fill, np.float32),
+            "K": np.full((cfg.pods, cfg.H, 9), 0.1, np.float32),
+            "mu": np.full(g, 0.2, np.float32), "sigma": np.full(g, 0.03, np.float32),
+            "M": np.tile(np.eye(cfg.H, dtype=np.float32), (cfg.pods, 1, 1))}
+
+
+@pytest.mark.parametrize("name,index", [("WP", 0), ("WI", -1), ("WV", 77), ("K", 5), ("M", 3),
+                                        ("mu", 1), ("sigma", -1)])
+@pytest.mark.parametrize("bad", [float("nan"), float("inf"), -float("inf")])
+def test_check_params_rejects_non_finite_entries(name, index, bad):
+    """slime_ca_check_params, the checks slime_ca_set_params makes before any upload:
+    every array of every pod, per-cell growth included, must be finite."""
+    lib = _lib.load()
+    cfg = _cfg(B=2, pods=2, growth_per_cell=int(name in ("mu", "sigma")))
+    arrs = _param_arrays(cfg)
+    p = _lib.Params(*[arrs[k].ctypes.data for k in ("WP", "WI", "WV", "K", "mu", "sigma", "M")])
+    assert lib.slime_ca_check_params(ctypes.byref(cfg), ctypes.byref(p)) == _lib.SLIME_OK
+    arrs[name].reshape(-1)[index] = bad
+    rc = lib.slime_ca_check_params(ctypes.byref(cfg), ctypes.byref(p))
+    assert rc == _lib.SLIME_EINVAL
+    assert name.encode() in lib.slime_ca_last_error() and b"finite" in lib.slime_ca_last_error()
+
+
+def test_check_params_rejects_null_and_invalid_config():
+    lib = _lib.load()
+    cfg = _cfg()
+    arrs = _param_arrays(cfg)
+    p = _lib.Params(*[arrs[k].ctypes.data for k in ("WP", "WI", "WV", "K", "mu", "sigma", "M")])
+    assert lib.slime_ca_check_params(None, ctypes.byref(p)) == _lib.SLIME_EINVAL
+    assert lib.slime_ca_check_params(ctypes.byref(cfg), None) == _lib.SLIME_EINVAL
+    p.K = None
+    assert lib.slime_ca_check_params(ctypes.byref(cfg), ctypes.byref(p)) == _lib.SLIME_EINVAL
+    assert lib.slime_ca_check_params(ctypes.byref(_cfg(G=12)), ctypes.byref(p)) == _lib.SLIME_EINVAL

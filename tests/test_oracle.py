@@ -64,6 +64,24 @@ def test_project_matches_numpy_matmul(oracle, D, pods, chain):
         assert norm_err(V[b].reshape(-1, cfg.C), rv) < 1e-6
 
 
+@pytest.mark.parametrize("pods", [1, 2])
+def test_project_perception_sum_matches_scipy_wrap_filter(oracle, pods):
+    """pvi_chain 2: P = ReLU(S W_P) with S = 9 x the 3 x 3 wrap-mode box mean of X
+    (scipy.ndimage.uniform_filter), then the chain I = GELU(P W_I), V = I W_V."""
+    cfg = OracleConfig(B=2, G=8, H=H, D=8, pods=pods, pvi_chain=2)
+    p, X = _params(cfg), _state(cfg)
+    P, I, V = oracle.project(cfg, X, p["WP"], p["WI"], p["WV"])
+    for b in range(cfg.B):
+        q = b // (cfg.B // pods)
+        S = 9.0 * ndimage.uniform_filter(X[b].astype(np.float64), size=(3, 3, 1), mode="wrap")
+        S = S.reshape(-1, cfg.C)
+        rp = np.maximum(S @ p["WP"][q].astype(np.float64), 0)
+        ri = _gelu(rp @ p["WI"][q].astype(np.float64))
+        rv = ri @ p["WV"][q].astype(np.float64)
+        for got, ref in ((P, rp), (I, ri), (V, rv)):
+            np.testing.assert_allclose(got[b].reshape(-1, cfg.C), ref, rtol=1e-5, atol=1e-6)
+
+
 def test_project_identity_weights(oracle):
     cfg = OracleConfig(B=1, G=8, H=H, D=8)
     X = _state(cfg) - 0.5

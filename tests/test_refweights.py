@@ -93,3 +93,52 @@ def test_short_slabs_are_rejected():
     wp, wi, wv, m, k = _reference_weights()
     with pytest.raises(ValueError):
         from_reference_weights(wp[:, :32], wi, wv, m, k)
+
+
+def _reference_head_neighbourhood(X, y, x, h, wp, wi, wv):
+    """As _reference_head, with the perception loop of pseudopod.cu:79-95 over the
+    3 x 3 neighbourhood (dy, dx outer, channel c inner, as the kernel runs it) and
+    the border wrapped (toroidal) where the kernel clamps."""
+    G = X.shape[1]
+    wp_f = np.asarray(wp, np.float64).ravel()
+    perception = np.zeros(D)
+    for i in range(D):
+        for dy in range(3):
+            for dx in range(3):
+                nb = X[0, (y + dy - 1) % G, (x + dx - 1) % G, h * D:(h + 1) * D].astype(np.float64)
+                for c in range(D):
+                    perception[i] += nb[c] * wp_f[h * CHANNELS * HIDDEN + c * HIDDEN + i]
+        perception[i] = max(0.0, perception[i])
+    wi_f, wv_f = (np.asarray(a, np.float64).ravel() for a in (wi, wv))
+    interaction = np.zeros(D)
+    for i in range(D):
+        for j in range(D):
+            interaction[i] += perception[j] * wi_f[h * CHANNELS * HIDDEN + j * HIDDEN + i]
+    interaction = _gelu_tanh(interaction)
+    output = np.zeros(D)
+    for i in range(D):
+        for j in range(HIDDEN):
+            output[i] += interaction[j % D] * wv_f[h * HIDDEN * CHANNELS + j * CHANNELS + i]
+    return perception, interaction, output
+
+
+def test_embedded_perception_chain_equals_reference_neighbourhood_loops(oracle):
+    """pvi_chain 2 (the 3 x 3 neighbourhood sum before the perception product) against
+    the reference kernel's own loops, at border cells, where the wrap matters, and an
+    interior one."""
+    wp, wi, wv, m, k = _reference_weights()
+    p = from_reference_weights(wp, wi, wv, m, k)
+    cfg = OracleConfig(B=1, G=8, H=H, D=D, pvi_chain=2)
+    X = np.random.default_rng(6).random((1, 8, 8, H * D), dtype=np.float32)
+    P, I, V = oracle.project(cfg, X, p["WP"], p["WI"], p["WV"])
+    for (y, x) in [(0, 0), (3, 5), (7, 2), (0, 7)]:
+        for h in (0, 5):
+            rp, ri, rv = _reference_head_neighbourhood(X, y, x, h, wp, wi, wv)
+            blk = slice(h * D, (h + 1) * D)
+            np.testing.assert_allclose(P[0, y, x, blk], rp, rtol=1e-5, atol=1e-6)
+            np.testing.assert_allclose(I[0, y, x, blk], ri, rtol=1e-5, atol=1e-6)
+            np.testing.assert_allclose(V[0, y, x, blk], rv, rtol=1e-5, atol=1e-6)
+    # and it differs from projecting the cell itself (pvi_chain 1)
+    P1, _, _ = oracle.project(OracleConfig(B=1, G=8, H=H, D=D, pvi_chain=1), X, p["WP"], p["WI"],
+                              p["WV"])
+    assert not np.allclose(P1, P, rtol=1e-2)

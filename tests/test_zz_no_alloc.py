@@ -84,3 +84,30 @@ def test_static_fitness_rejects_what_does_not_fit():
     assert b"static scratch" in lib.slime_ca_last_error()
     rc = lib.slime_ca_fitness_static(ctypes.byref(c), p, 1, p, p, p, ctypes.c_void_p(0))  # T < 2
     assert rc == _lib.SLIME_EINVAL
+
+
+def test_static_fitness_calls_on_two_streams_are_ordered():
+    """Two calls back to back on two streams, with no synchronisation between them:
+    the second waits for the first's event before its kernels write the shared
+    scratch, so both results equal slime_ca_fitness's."""
+    cfg_a = CAConfig("nalloc-a", B=4, G=32, H=8, D=64, dtype="bf16", steps=1, w_std=0.05, blobs=True)
+    cfg_b = CAConfig("nalloc-b", B=2, G=32, H=8, D=64, dtype="bf16", steps=1, w_std=0.05)
+    print("[case] slime_ca_fitness_static on two streams", flush=True)
+    ha, hb = _history(cfg_a, 8, 5), _history(cfg_b, 6, 9)
+    ref_a, ref_b = _handle_fitness(cfg_a, ha), _handle_fitness(cfg_b, hb)
+    lib = _lib.load()
+    outs = []
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    torch.cuda.synchronize()
+    for cfg, hist, st in ((cfg_a, ha, streams[0]), (cfg_b, hb, streams[1])):
+        c = _lib.Config(cfg.B, cfg.G, cfg.H, cfg.D, _lib.SLIME_BF16, cfg.dt, 0, 1, 0)
+        o = [torch.full((cfg.B, cfg.H), float("nan"), dtype=torch.float32, device="cuda") for _ in range(3)]
+        rc = lib.slime_ca_fitness_static(ctypes.byref(c), ctypes.c_void_p(hist.data_ptr()),
+                                         int(hist.shape[0]), *[ctypes.c_void_p(t.data_ptr()) for t in o],
+                                         ctypes.c_void_p(st.cuda_stream))
+        _lib.check(rc)
+        outs.append(o)
+    torch.cuda.synchronize()
+    for got, ref in ((outs[0], ref_a), (outs[1], ref_b)):
+        for name, g, r in zip(("erank", "coherence", "fitness"), got, ref):
+            np.testing.assert_array_equal(g.cpu().numpy(), r, err_msg=name)
