@@ -114,6 +114,81 @@ def cpu_baseline(cfg, params, X, seconds: float):
     }
 
 
+# ---- rocprofv3 kernel-trace summaries ------------------------------------------------
+# Algorithmic work per launch of the kernels of each workload: ("B", bytes) for an
+# HBM-bound kernel, ("F", flops) for a matrix-core one, per cell of the launch
+# (1,048,576 cells in c3 and c5). Reads and writes are counted once per cell.
+def _trace_work(workload: str) -> dict:
+    C = 512
+    if workload == "c3":
+        return {
+            "gemm_mfma_kernel<unsigned short>": ("[P\\|I\\|V] projection GEMM", "F", 2 * C * 3 * C),
+            "stencil_mfma_kernel<unsigned short>": ("S2-S6 + mass partials, bf16 out", "B", 5 * C * 2),
+            "stencil_mfma_kernel<float>": ("last step of a call, fp32 out", "B", 4 * C * 2 + C * 4),
+            "rescale_kernel<float, unsigned short>": ("final rescale, fp32 -> bf16", "B", C * 4 + C * 2),
+            "weight_prep_kernel<unsigned short>": ("per-batch scaled weights", None, None),
+            "mass_finalize_kernel": ("S7 factors", None, None),
+        }
+    if workload == "c5":
+        return {
+            "bw_cell_kernel<unsigned short, 64>": (
+                "S7-S4 per (cell, head), tape for the gathers", "B",
+                5 * C * 2 + C * 4 + 3 * C * 4 + C * 2 + 2 * 8 * 9 * 4),
+            "bw_gather_tile_kernel<unsigned short>": (
+                "gV, gI~, potential transpose", "B", 3 * C * 4 + 2 * C * 2 + 2 * 8 * 9 * 4 + 2 * C * 2 + C * 4),
+            "gemm_mfma_add_kernel<unsigned short>": ("dX GEMM + direct part", "F", 2 * C * 3 * C),
+            "bw_dw_mfma2_kernel": ("weight gradients", "F", 2 * C * 3 * C),
+            "gemm_mfma_kernel<unsigned short>": ("tape projections, I before GELU, forward", None, None),
+            "stencil_mfma_kernel<float>": ("tape step, fp32 out", "B", 4 * C * 2 + C * 4),
+            "stencil_mfma_kernel<unsigned short>": ("forward step", "B", 5 * C * 2),
+            "bw_loss_partial_kernel<unsigned short>": ("loss partials", "B", C * 4 + C * 2),
+        }
+    return {}
+
+
+def _short_name(full: str) -> str:
+    name = full.replace("void ", "", 1)
+    for pre in ("slime::(anonymous namespace)::", "slime::"):
+        name = name.replace(pre, "")
+    return name.split("(")[0].strip()
+
+
+def trace_summary(path: str, workload: str, cells: int = 1 << 20) -> str:
+    """Markdown table of a rocprofv3 --stats kernel CSV: calls and durations of each
+    kernel and, for the kernels of `workload` with a known algorithmic work, the
+    achieved rate and its fraction of the MI355X peak."""
+    import csv
+    work = _trace_work(workload)
+    rows = []
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            rows.append((_short_name(r["Name"]), int(r["Calls"]), float(r["AverageNs"]),
+                         float(r["TotalDurationNs"]), float(r["Percentage"]), float(r["MinNs"]),
+                         float(r["MaxNs"])))
+    lines = ["| kernel | what | calls | avg µs | min µs | max µs | total ms | % GPU time | "
+             "work per launch | achieved | of peak |",
+             "|---|---|---|---|---|---|---|---|---|---|---|"]
+    for name, calls, avg, tot, pct, mn, mx in sorted(rows, key=lambda r: -r[3]):
+        if name not in work:
+            continue
+        what, kind, per_cell = work[name]
+        cols = [f"`{name}`", what, str(calls), f"{avg / 1e3:.1f}", f"{mn / 1e3:.1f}", f"{mx / 1e3:.1f}",
+                f"{tot / 1e6:.2f}", f"{pct:.2f}"]
+        if kind == "B":
+            b = per_cell * cells
+            rate = b / (avg * 1e-9) / 1e12
+            cols += [f"{b / 1e9:.3f} GB", f"{rate:.2f} TB/s", f"{rate * 1e3 / PEAK_HBM_GBS:.1%} of 8 TB/s"]
+        elif kind == "F":
+            fl = per_cell * cells
+            rate = fl / (avg * 1e-9) / 1e12
+            cols += [f"{fl:.4g} flop", f"{rate:.0f} TFLOP/s",
+                     f"{rate / PEAK_TFLOPS['bf16']:.1%} of 2.5 PFLOP/s"]
+        else:
+            cols += ["-", "-", "-"]
+        lines.append("| " + " | ".join(cols) + " |")
+    return "\n".join(lines)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -126,7 +201,13 @@ def main() -> int:
                     help="time the c5 gradient (slime_ca_backward) instead of the headline")
     ap.add_argument("--ensemble", action="store_true",
                     help="time the c4 ensemble: 16 pods' steps and the fused fitness")
+    ap.add_argument("--trace-summary", metavar="CSV",
+                    help="print a markdown roofline table of a rocprofv3 kernel_stats.csv "
+                         "(no GPU needed) for --config c3 or c5, then exit")
     args = ap.parse_args()
+    if args.trace_summary:
+        print(trace_summary(args.trace_summary, args.config))
+        return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported in this "
               "build (the path shards by batch with no collective)",
