@@ -84,6 +84,18 @@ typedef struct {
                                of X, the perception of multi_head_ca_kernel
                                (slime/core/pseudopod.cu:62-91, which clamps at the
                                border instead of wrapping) */
+    int growth_fn;       /* S3: 0 the bell 2 exp(-((U-mu)/(sigma+1e-7))^2) - 1
+                               (failed_attempts/warp_ca.cu:49-56);
+                            1 the Gaussian exp(-(U-mu)^2 / (2 sigma^2))
+                               (failed_attempts/pseudopod.cu:46-48; sigma != 0);
+                            2 the shipped U exp(-U^2), mu and sigma unused
+                               (slime/core/pseudopod.cu:183) */
+    int conservation;    /* S7: 0 per (batch, head) over the grid
+                               (failed_attempts/warp_ca.cu:401-450);
+                            1 per (cell, head) first, the shipped kernel's
+                               renormalisation (slime/core/pseudopod.cu:160-165,
+                               196-203), then per (batch, head) as 0 (a factor of 1
+                               up to rounding) */
 } slime_ca_config;
 
 typedef struct {
@@ -161,7 +173,7 @@ typedef struct {
  * NULL) receives L, which synchronises the stream. No counterpart in the
  * reference: it declares gradients (gradients_d and update_gradients,
  * slime/proto/model.cu:7,13) but never computes them. SLIME_EINVAL for chained
- * projections. */
+ * projections, growth_fn != 0 or conservation != 0. */
 int slime_ca_backward(slime_ca* ca, const void* x_in, const void* target, float* grad_x,
                       const slime_ca_grads* grads, double* loss, void* hip_stream);
 

@@ -32,6 +32,8 @@ class _Cfg(ctypes.Structure):
         ("growth_per_cell", ctypes.c_int),
         ("pvi_chain", ctypes.c_int),
         ("dt", ctypes.c_float),
+        ("growth_fn", ctypes.c_int),
+        ("conservation", ctypes.c_int),
     ]
 
 
@@ -45,6 +47,8 @@ class OracleConfig:
     growth_per_cell: bool = False
     pvi_chain: int = 0  # 0 parallel, 1 chained, 2 chained with the 3x3 perception sum
     dt: float = 0.1
+    growth_fn: int = 0  # 0 bell, 1 Gaussian, 2 shipped U exp(-U^2)
+    conservation: int = 0  # 0 per (b, head); 1 per (cell, head) first
 
     @property
     def C(self) -> int:
@@ -52,7 +56,7 @@ class OracleConfig:
 
     def c(self) -> _Cfg:
         return _Cfg(self.B, self.G, self.H, self.D, self.pods, int(self.growth_per_cell),
-                    int(self.pvi_chain), self.dt)
+                    int(self.pvi_chain), self.dt, int(self.growth_fn), int(self.conservation))
 
 
 def build() -> str:

@@ -12,7 +12,9 @@
 //   S2 potential     slime/core/pseudopod.cu:168-180 (per-head 3x3 flow kernel),
 //                    toroidal wrap as slime/kernels/warp_ca.cu:305-310 and
 //                    slime/kernels/triton_impl.cu:90-105
-//   S3 growth        failed_attempts/warp_ca.cu:49-56
+//   S3 growth        failed_attempts/warp_ca.cu:49-56; variants: the Gaussian of
+//                    failed_attempts/pseudopod.cu:46-48 and the shipped U exp(-U^2)
+//                    of slime/core/pseudopod.cu:183
 //   S4 activation    failed_attempts/pseudopod.cu:208-251 (query = centre
 //                    perception, key = neighbour interaction, /sqrt(dim),
 //                    max-subtracted softmax)
@@ -22,7 +24,9 @@
 //                    failed_attempts/pseudopod.cu:330 (dt*(growth*value)),
 //                    slime/core/pseudopod.cu:231-251 (head mixing M[o][h])
 //   S7 conservation  failed_attempts/warp_ca.cu:401-450 (global sum rescale),
-//                    slime/core/pseudopod.cu:21,198 (|mass| > 1e-6 guard)
+//                    slime/core/pseudopod.cu:21,198 (|mass| > 1e-6 guard); variant:
+//                    the shipped per-cell, per-head renormalisation of
+//                    slime/core/pseudopod.cu:160-165,196-203
 //   E1 Gram          failed_attempts/pseudopod.cu:366-384 (d x d correlation
 //                    over all cells; here per head, not averaged over heads)
 //   E2 Jacobi        failed_attempts/pseudopod.cu:391-436 (cyclic two-sided
@@ -56,6 +60,8 @@ struct Dims {
 
 bool dims_of(const oracle_ca_cfg* cfg, Dims* d) {
     if (!cfg || cfg->B <= 0 || cfg->G <= 0 || cfg->H <= 0 || cfg->D <= 0 || cfg->pods <= 0)
+        return false;
+    if (cfg->growth_fn < 0 || cfg->growth_fn > 2 || cfg->conservation < 0 || cfg->conservation > 1)
         return false;
     if (cfg->B % cfg->pods != 0) return false;
     d->B = cfg->B;
@@ -168,7 +174,17 @@ void potential(const Dims& d, const double* X, const float* K, double* U) {
         }
 }
 
-void growth(const Dims& d, int per_cell, const double* U, const float* mu, const float* sigma,
+// fn 0: the bell 2 exp(-((U - mu) / (sigma + 1e-7))^2) - 1 (failed_attempts/warp_ca.cu:49-56);
+// fn 1: the Gaussian exp(-(U - mu)^2 / (2 sigma^2)) (failed_attempts/pseudopod.cu:46-48);
+// fn 2: the shipped kernel's U exp(-U^2), no mu or sigma (slime/core/pseudopod.cu:183).
+double growth_of(int fn, double u, double m, double s) {
+    if (fn == 1) return std::exp(-(u - m) * (u - m) / (2.0 * s * s));
+    if (fn == 2) return u * std::exp(-u * u);
+    const double z = (u - m) / (s + 1e-7);
+    return 2.0 * std::exp(-z * z) - 1.0;
+}
+
+void growth(const Dims& d, int per_cell, int fn, const double* U, const float* mu, const float* sigma,
             double* g) {
     const int C = d.C, D = d.D;
 #pragma omp parallel for schedule(static)
@@ -180,10 +196,8 @@ void growth(const Dims& d, int per_cell, const double* U, const float* mu, const
             const size_t pi = per_cell ? ((size_t)pod * d.cells + cell) * d.H + h
                                        : (size_t)pod * d.H + h;
             const double m = mu[pi], s = sigma[pi];
-            for (int c = 0; c < D; ++c) {
-                const double z = (U[(size_t)r * C + h * D + c] - m) / (s + 1e-7);
-                g[(size_t)r * C + h * D + c] = 2.0 * std::exp(-z * z) - 1.0;
-            }
+            for (int c = 0; c < D; ++c)
+                g[(size_t)r * C + h * D + c] = growth_of(fn, U[(size_t)r * C + h * D + c], m, s);
         }
     }
 }
@@ -265,9 +279,33 @@ void mix(const Dims& d, double dt, const double* X, const double* g, const doubl
     }
 }
 
-// Per (b, head o): Y_o *= sum(X_o) / sum(Y_o) unless |sum(Y_o)| <= 1e-6.
-void conserve(const Dims& d, const double* X, double* Y, double* mass_in, double* mass_out) {
+// Per (cell, head o), the shipped kernel's renormalisation (slime/core/pseudopod.cu:
+// 160-165, 196-203): Y_o(cell) *= sum_c X_o(cell) / sum_c Y_o(cell) unless the
+// latter is at most 1e-6 in magnitude. Applied to the mixed output, so that each
+// cell's head sums equal its input's.
+void conserve_cells(const Dims& d, const double* X, double* Y) {
     const int C = d.C, D = d.D, H = d.H;
+#pragma omp parallel for schedule(static)
+    for (long r = 0; r < (long)d.B * d.cells; ++r)
+        for (int o = 0; o < H; ++o) {
+            const size_t base = (size_t)r * C + o * D;
+            double sx = 0.0, sy = 0.0;
+            for (int c = 0; c < D; ++c) {
+                sx += X[base + c];
+                sy += Y[base + c];
+            }
+            if (std::fabs(sy) > 1e-6)
+                for (int c = 0; c < D; ++c) Y[base + c] *= sx / sy;
+        }
+}
+
+// Per (b, head o): Y_o *= sum(X_o) / sum(Y_o) unless |sum(Y_o)| <= 1e-6. With
+// per_cell set, the per-cell renormalisation runs first (the global factor is then
+// 1 up to rounding, unless a cell's sum took the guard).
+void conserve(const Dims& d, int per_cell, const double* X, double* Y, double* mass_in,
+              double* mass_out) {
+    const int C = d.C, D = d.D, H = d.H;
+    if (per_cell) conserve_cells(d, X, Y);
     for (int b = 0; b < d.B; ++b)
         for (int o = 0; o < H; ++o) {
             double sx = 0.0, sy = 0.0;
@@ -342,7 +380,7 @@ int oracle_growth(const oracle_ca_cfg* cfg, const float* U, const float* mu, con
     if (!dims_of(cfg, &d)) return -1;
     const size_t n = (size_t)d.B * d.cells * d.C;
     std::vector<double> ud = to_d(U, n), gd(n);
-    growth(d, cfg->growth_per_cell, ud.data(), mu, sigma, gd.data());
+    growth(d, cfg->growth_per_cell, cfg->growth_fn, ud.data(), mu, sigma, gd.data());
     to_f(gd, g);
     return 0;
 }
@@ -384,7 +422,7 @@ int oracle_conserve(const oracle_ca_cfg* cfg, const float* X, float* Y, double* 
     if (!dims_of(cfg, &d)) return -1;
     const size_t n = (size_t)d.B * d.cells * d.C;
     std::vector<double> xd = to_d(X, n), yd = to_d(Y, n);
-    conserve(d, xd.data(), yd.data(), mass_in, mass_out);
+    conserve(d, cfg->conservation, xd.data(), yd.data(), mass_in, mass_out);
     to_f(yd, Y);
     return 0;
 }
@@ -400,11 +438,11 @@ int oracle_step(const oracle_ca_cfg* cfg, const float* X_in, const float* WP, co
     for (int s = 0; s < n_steps; ++s) {
         project_all(d, cfg->pvi_chain, x.data(), WP, WI, WV, P.data(), I.data(), V.data());
         potential(d, x.data(), K, U.data());
-        growth(d, cfg->growth_per_cell, U.data(), mu, sigma, g.data());
+        growth(d, cfg->growth_per_cell, cfg->growth_fn, U.data(), mu, sigma, g.data());
         attention(d, P.data(), I.data(), A.data());
         propagate(d, A.data(), V.data(), Vt.data());
         mix(d, cfg->dt, x.data(), g.data(), Vt.data(), M, Y.data());
-        conserve(d, x.data(), Y.data(), mass_in, mass_out);
+        conserve(d, cfg->conservation, x.data(), Y.data(), mass_in, mass_out);
         // The state is carried between steps in fp32, as the fp32 device path does.
         for (size_t i = 0; i < n; ++i) x[i] = (double)(float)Y[i];
     }
@@ -613,7 +651,7 @@ int oracle_step_backward(const oracle_ca_cfg* cfg, const float* X_in, const floa
                          float* gX, float* gWP, float* gWI, float* gWV, float* gK, float* gmu,
                          float* gsigma, float* gM) {
     Dims d;
-    if (!dims_of(cfg, &d) || cfg->pvi_chain || !loss) return -1;
+    if (!dims_of(cfg, &d) || cfg->pvi_chain || cfg->growth_fn || cfg->conservation || !loss) return -1;
     const int G = d.G, C = d.C, D = d.D, H = d.H;
     const int per_cell = cfg->growth_per_cell;
     const double dt = cfg->dt, inv_sqrt_d = 1.0 / std::sqrt((double)D);
@@ -630,7 +668,7 @@ int oracle_step_backward(const oracle_ca_cfg* cfg, const float* X_in, const floa
         I[i] = gelu_tanh(it[i]);
     }
     potential(d, x.data(), K, U.data());
-    growth(d, per_cell, U.data(), mu, sigma, g.data());
+    growth(d, per_cell, 0, U.data(), mu, sigma, g.data());
     attention(d, P.data(), I.data(), A.data());
     propagate(d, A.data(), V.data(), Vt.data());
     mix(d, dt, x.data(), g.data(), Vt.data(), M, Y.data());

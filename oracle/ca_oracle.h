@@ -31,6 +31,8 @@ typedef struct {
     int growth_per_cell;
     int pvi_chain; /* 0 parallel; 1 chained; 2 chained, P from the 3x3 neighbourhood sum */
     float dt;
+    int growth_fn;    /* 0 bell, 1 Gaussian, 2 shipped U exp(-U^2) */
+    int conservation; /* 0 per (b, head); 1 per (cell, head), then per (b, head) */
 } oracle_ca_cfg;
 
 /* Each returns 0 on success, -1 on invalid configuration. */

@@ -38,7 +38,8 @@ class Config(ctypes.Structure):
     _fields_ = [("B", ctypes.c_int), ("G", ctypes.c_int), ("H", ctypes.c_int),
                 ("D", ctypes.c_int), ("dtype", ctypes.c_int), ("dt", ctypes.c_float),
                 ("growth_per_cell", ctypes.c_int), ("pods", ctypes.c_int),
-                ("pvi_chain", ctypes.c_int)]
+                ("pvi_chain", ctypes.c_int), ("growth_fn", ctypes.c_int),
+                ("conservation", ctypes.c_int)]
 
 
 class Params(ctypes.Structure):

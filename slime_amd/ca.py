@@ -40,11 +40,17 @@ class Pseudopod:
     ``pvi_chain``: 0 computes P, I and V from the state; 1 chains them (I from P,
     V from I, slime/core/pseudopod.cu:98-119); 2 chains them with P from the 3x3
     neighbourhood sum of the state, the perception of multi_head_ca_kernel
-    (slime/core/pseudopod.cu:62-91, toroidal here)."""
+    (slime/core/pseudopod.cu:62-91, toroidal here).
+
+    ``growth_fn``: 0 the bell growth (failed_attempts/warp_ca.cu:49-56), 1 the
+    Gaussian (failed_attempts/pseudopod.cu:46-48), 2 the shipped U exp(-U^2)
+    (slime/core/pseudopod.cu:183). ``conservation``: 0 per (batch, head), 1 per
+    (cell, head) first, as the shipped kernel renormalises
+    (slime/core/pseudopod.cu:160-165,196-203)."""
 
     def __init__(self, B: int, G: int, H: int = 8, D: int = 64, dtype: str = "bf16",
                  dt: float = 0.1, growth_per_cell: bool = False, pods: int = 1,
-                 pvi_chain: int = 0):
+                 pvi_chain: int = 0, growth_fn: int = 0, conservation: int = 0):
         if dtype not in _DTYPES:
             raise ValueError(f"dtype must be one of {sorted(_DTYPES)}")
         self.lib = _lib.load()
@@ -54,7 +60,7 @@ class Pseudopod:
         self.pods = pods
         self.growth_per_cell = growth_per_cell
         cfg = _lib.Config(B, G, H, D, _DTYPES[dtype], dt, int(growth_per_cell), pods,
-                          int(pvi_chain))
+                          int(pvi_chain), int(growth_fn), int(conservation))
         handle = ctypes.c_void_p()
         _lib.check(self.lib.slime_ca_create(ctypes.byref(cfg), ctypes.byref(handle)))
         self._h = handle

@@ -140,6 +140,9 @@ int validate(const slime_ca_config* c) {
     if (c->growth_per_cell != 0 && c->growth_per_cell != 1)
         return fail(SLIME_EINVAL, "growth_per_cell must be 0 or 1");
     if (c->pvi_chain < 0 || c->pvi_chain > 2) return fail(SLIME_EINVAL, "pvi_chain must be 0, 1 or 2");
+    if (c->growth_fn < 0 || c->growth_fn > 2) return fail(SLIME_EINVAL, "growth_fn must be 0, 1 or 2");
+    if (c->conservation != 0 && c->conservation != 1)
+        return fail(SLIME_EINVAL, "conservation must be 0 or 1");
     const double elems = (double)c->B * c->G * c->G * c->H * c->D;
     if (elems > 4.0e9) return fail(SLIME_EINVAL, "state of %.3g elements is too large", elems);
     // The stencils address one batch entry with 32-bit offsets: element offsets in
@@ -305,7 +308,10 @@ int run_stencil(slime_ca* h, const void* x, const float* x_scale, const void* P,
     a.per_pod = c.B / c.pods;
     a.per_cell = c.growth_per_cell;
     a.dt = c.dt;
+    a.growth_fn = c.growth_fn;
     HIP_TRY(timed(h, h->stencil_ev, s, [&] { return launch_stencil(c.dtype, a, s); }));
+    if (c.conservation == 1)
+        HIP_TRY(launch_cell_conserve(c.dtype, x, x_scale, y_raw, y_f32, h->part_out, c.B, c.G, c.D, s));
     HIP_TRY(launch_mass_finalize(h->part_in, h->part_out, c.B * c.H, h->tiles, h->mass_in,
                                  h->mass_out, out_scale, out_scale64, s));
     return SLIME_OK;
@@ -464,6 +470,10 @@ int slime_ca_check_params(const slime_ca_config* config, const slime_ca_params* 
         for (size_t i = 0; i < a.n; ++i)
             if (!std::isfinite(a.v[i]))
                 return fail(SLIME_EINVAL, "%s entry %zu is not finite", a.name, i);
+    if (c.growth_fn == 1)  // the Gaussian divides by 2 sigma^2
+        for (size_t i = 0; i < ng; ++i)
+            if (p->sigma[i] == 0.f)
+                return fail(SLIME_EINVAL, "sigma entry %zu is zero (Gaussian growth)", i);
     return SLIME_OK;
 }
 
@@ -805,6 +815,8 @@ int slime_ca_backward(slime_ca* h, const void* x_in, const void* target, float* 
     if (!x_in || !target || !grad_x) return fail(SLIME_EINVAL, "a tensor pointer is NULL");
     const slime_ca_config& c = h->cfg;
     if (c.pvi_chain) return fail(SLIME_EINVAL, "the backward supports parallel projections only");
+    if (c.growth_fn || c.conservation)
+        return fail(SLIME_EINVAL, "the backward supports the bell growth and global conservation only");
     const size_t C = h->C, BH = (size_t)c.B * c.H, n = (size_t)h->state_elems;
     const size_t cells = (size_t)c.B * c.G * c.G;
     const int lchunks = backward_loss_chunks(c.G);

@@ -112,6 +112,17 @@ __device__ __forceinline__ double wave_sum64(double v) {
     return (readlane_f64(v, 0) + readlane_f64(v, 16)) + (readlane_f64(v, 32) + readlane_f64(v, 48));
 }
 
+// Sum over aligned groups of kN consecutive lanes (kN = 1, 2, 4 or 8), every lane of
+// the group receiving the group's sum (DPP quad_perm and row_half_mirror steps).
+template <int kN>
+__device__ __forceinline__ float group_sum_n(float v) {
+    static_assert(kN == 1 || kN == 2 || kN == 4 || kN == 8, "group of 1, 2, 4 or 8 lanes");
+    if constexpr (kN >= 2) v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
+    if constexpr (kN >= 4) v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]
+    if constexpr (kN >= 8) v += dpp_f32<0x141>(v);  // row_half_mirror
+    return v;
+}
+
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float rcp_fast(float x) { return __builtin_amdgcn_rcpf(x); }
 

@@ -77,6 +77,7 @@ struct StencilArgs {
     double* part_out;        // [B][H][tiles]  sum of stored Y per tile
     int B, G, D, per_pod, per_cell;
     float dt;
+    int growth_fn;           // 0 bell, 1 Gaussian, 2 U exp(-U^2) (growth_args, stencil.hip)
 };
 int stencil_tiles_per_batch(int G);
 // Host-side table for StencilArgs::kband: bytes for `pods` pods, and its contents
@@ -96,6 +97,13 @@ hipError_t launch_mass_finalize(const double* part_in, const double* part_out, i
                                 double* mass_in, double* mass_out, float* scale_out,
                                 double* scale64_out, hipStream_t s);
 hipError_t launch_fill_f64(double* p, int n, double v, hipStream_t s);
+// Conservation 1 (per cell and head, slime/core/pseudopod.cu:160-165,196-203), between
+// the stencil and launch_mass_finalize: y (the stencil's unscaled output, fp32 when
+// y_f32 is set, else the storage type) is renormalised in place per (cell, head) to
+// the head sum of x scaled by `scale` ([2][B][H], nullptr = 1), and the per-tile sums
+// of part_out ([B][H][tiles], the stencil's layout) are rewritten from the result.
+hipError_t launch_cell_conserve(int dtype, const void* x, const float* scale, void* y, int y_f32,
+                                double* part_out, int B, int G, int D, hipStream_t s);
 // y[i] = cvt((scale[0][b][h] + scale[1][b][h]) * x[i]) over the whole state; x is
 // fp32 when x_f32 is set, else in the storage type.
 hipError_t launch_rescale(int dtype, const void* x, int x_f32, const float* scale, void* y, int B,

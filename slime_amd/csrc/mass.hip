@@ -127,6 +127,93 @@ hipError_t launch_fill_f64(double* p, int n, double v, hipStream_t s) {
     return hipGetLastError();
 }
 
+// ---- conservation 1: the shipped kernel's per-(cell, head) renormalisation ----------------
+// slime/core/pseudopod.cu:160-165,196-203 renormalises each cell's head to the mass it
+// had before the update: Y_o(cell) *= sum_c Xs_o(cell) / sum_c Y_o(cell), skipped when
+// |sum_c Y_o(cell)| <= 1e-6 (MASS_CONSERVATION_EPSILON, :21). Xs is the state with its
+// deferred per-(b, head) factor applied (hi + lo), as the stencil reads it. One
+// workgroup per stencil tile (4 x 8 cells) rewrites that tile's part_out sums from the
+// renormalised values, so the per-(b, head) factor S7 then computes from the partials
+// is 1 up to rounding (or corrects the cells the guard skipped).
+namespace {
+constexpr int kCcTileY = 4, kCcTileX = 8, kCcCells = kCcTileY * kCcTileX;
+
+template <typename TX, typename TY, int D>
+__global__ __launch_bounds__(256) void cell_conserve_kernel(const TX* X, const float* scale_in, TY* Y,
+                                                            double* part_out, int B, int G) {
+    constexpr int C = kHeads * D, U = C / 8;  // 8-channel units per cell; D / 8 per head
+    __shared__ double sR[256];
+    const int tiles_x = G / kCcTileX, tpb = (G / kCcTileY) * tiles_x;
+    const int b = blockIdx.x / tpb, tile = blockIdx.x % tpb;
+    const int ty0 = (tile / tiles_x) * kCcTileY, tx0 = (tile % tiles_x) * kCcTileX;
+    const int tid = threadIdx.x;
+    const int j = tid % U, h = 8 * j / D;  // every unit of this thread is unit j of its cell
+    const float s_hi = scale_in ? scale_in[b * kHeads + h] : 1.0f;
+    const float s_lo = scale_in ? scale_in[B * kHeads + b * kHeads + h] : 0.0f;
+    float ysum = 0.f;
+    for (int u = tid; u < kCcCells * U; u += 256) {
+        const int cell = u / U;
+        const long long e = (((long long)b * G + ty0 + cell / kCcTileX) * G + tx0 + cell % kCcTileX) * C + 8 * j;
+        float xv[8], yv[8];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float2 x2 = Store<TX>::load2(X + e + 2 * q);
+            const float2 y2 = Store<TY>::load2(Y + e + 2 * q);
+            xv[2 * q] = x2.x, xv[2 * q + 1] = x2.y;
+            yv[2 * q] = y2.x, yv[2 * q + 1] = y2.y;
+        }
+        float sx = 0.f, sy = 0.f;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            sx += __builtin_fmaf(xv[q], s_lo, xv[q] * s_hi);
+            sy += yv[q];
+        }
+        // the D / 8 consecutive lanes of one (cell, head) share their sums
+        sx = group_sum_n<D / 8>(sx);
+        sy = group_sum_n<D / 8>(sy);
+        const float f = fabsf(sy) > 1e-6f ? sx / sy : 1.0f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float r0 = Store<TY>::round(yv[2 * q] * f), r1 = Store<TY>::round(yv[2 * q + 1] * f);
+            Store<TY>::store2(Y + e + 2 * q, r0, r1);
+            ysum += r0 + r1;
+        }
+    }
+    sR[tid] = ysum;
+    __syncthreads();
+    if (tid < kHeads) {  // head tid's threads, added in thread order
+        double s = 0.0;
+        for (int t = 0; t < 256; ++t)
+            if (8 * (t % U) / D == tid) s += sR[t];
+        part_out[((long long)b * kHeads + tid) * tpb + tile] = s;
+    }
+}
+
+template <typename TX, typename TY>
+hipError_t launch_cc_t(const void* x, const float* scale, void* y, double* part_out, int B, int G, int D,
+                       hipStream_t s) {
+    const dim3 grid((unsigned)(B * (G / kCcTileY) * (G / kCcTileX)));
+    const TX* xp = static_cast<const TX*>(x);
+    TY* yp = static_cast<TY*>(y);
+    switch (D) {
+        case 8: hipLaunchKernelGGL((cell_conserve_kernel<TX, TY, 8>), grid, dim3(256), 0, s, xp, scale, yp, part_out, B, G); break;
+        case 16: hipLaunchKernelGGL((cell_conserve_kernel<TX, TY, 16>), grid, dim3(256), 0, s, xp, scale, yp, part_out, B, G); break;
+        case 32: hipLaunchKernelGGL((cell_conserve_kernel<TX, TY, 32>), grid, dim3(256), 0, s, xp, scale, yp, part_out, B, G); break;
+        case 64: hipLaunchKernelGGL((cell_conserve_kernel<TX, TY, 64>), grid, dim3(256), 0, s, xp, scale, yp, part_out, B, G); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+}  // namespace
+
+hipError_t launch_cell_conserve(int dtype, const void* x, const float* scale, void* y, int y_f32,
+                                double* part_out, int B, int G, int D, hipStream_t s) {
+    if (dtype == 1)
+        return y_f32 ? launch_cc_t<bf16_t, float>(x, scale, y, part_out, B, G, D, s)
+                     : launch_cc_t<bf16_t, bf16_t>(x, scale, y, part_out, B, G, D, s);
+    return launch_cc_t<float, float>(x, scale, y, part_out, B, G, D, s);
+}
+
 hipError_t launch_rescale(int dtype, const void* x, int x_f32, const float* scale, void* y, int B,
                           int G, int C, int D, hipStream_t s) {
     const long long cells = (long long)G * G;

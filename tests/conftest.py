@@ -49,3 +49,32 @@ def peaked_params(cfg, seed=1):
     for k, s in (("WP", PEAKED_QK_STD), ("WI", PEAKED_QK_STD), ("WV", PEAKED_V_STD)):
         p[k] = rng.normal(0.0, s, p[k].shape).astype(np.float32)
     return p
+
+
+def growth_variant_params(cfg, oracle, X, seed=1, k_std=0.3):
+    """Parameters for the growth-function cases: make_params(cfg, seed) with the
+    3x3 kernels drawn from N(0, k_std), the value weights from N(0, PEAKED_V_STD)
+    (so the growth-modulated update is a visible share of Y), and mu, sigma set from
+    the potential U of
+    the state X itself (per head, or per cell and head): mu its mean and sigma its
+    standard deviation over the cells (over the channels, per cell). U then spans
+    the growth functions' active range, so the bell, the Gaussian and the shipped
+    U exp(-U^2) give visibly different updates."""
+    from slime_amd import make_params
+    p = make_params(cfg, seed=seed)
+    rng = np.random.default_rng(seed + 2000)
+    p["K"] = rng.normal(0.0, k_std, p["K"].shape).astype(np.float32)
+    p["WV"] = rng.normal(0.0, PEAKED_V_STD, p["WV"].shape).astype(np.float32)
+    ocfg = oracle.OracleConfig(B=cfg.B, G=cfg.G, H=cfg.H, D=cfg.D, pods=cfg.pods)
+    U = oracle.potential(ocfg, X, p["K"]).astype(np.float64)
+    U = U.reshape(cfg.B, cfg.G, cfg.G, cfg.H, cfg.D)
+    per = cfg.B // cfg.pods
+    if cfg.growth_per_cell:
+        mu = np.stack([U[q * per:(q + 1) * per].mean(axis=(0, 4)) for q in range(cfg.pods)])
+        sg = np.stack([U[q * per:(q + 1) * per].std(axis=(0, 4)) for q in range(cfg.pods)]) + 0.05
+    else:
+        mu = np.stack([U[q * per:(q + 1) * per].mean(axis=(0, 1, 2, 4)) for q in range(cfg.pods)])
+        sg = np.stack([U[q * per:(q + 1) * per].std(axis=(0, 1, 2, 4)) for q in range(cfg.pods)])
+    p["mu"] = mu.astype(np.float32)
+    p["sigma"] = sg.astype(np.float32)
+    return p

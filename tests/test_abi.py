@@ -38,7 +38,8 @@ def _cfg(**kw):
 
 @pytest.mark.parametrize("bad", [dict(B=0), dict(G=12), dict(G=4), dict(H=4), dict(D=48),
                                  dict(dtype=7), dict(pods=3), dict(dt=float("nan")),
-                                 dict(growth_per_cell=2), dict(pvi_chain=5)])
+                                 dict(growth_per_cell=2), dict(pvi_chain=5), dict(pvi_chain=3),
+                                 dict(growth_fn=3), dict(growth_fn=-1), dict(conservation=2)])
 def test_create_rejects_invalid_config(bad):
     lib = _lib.load()
     h = ctypes.c_void_p()
@@ -165,6 +166,17 @@ def test_check_params_rejects_non_finite_entries(name, index, bad):
     rc = lib.slime_ca_check_params(ctypes.byref(cfg), ctypes.byref(p))
     assert rc == _lib.SLIME_EINVAL
     assert name.encode() in lib.slime_ca_last_error() and b"finite" in lib.slime_ca_last_error()
+
+
+def test_check_params_rejects_zero_sigma_for_the_gaussian_growth_only():
+    lib = _lib.load()
+    for fn, ok in ((0, True), (1, False), (2, True)):
+        cfg = _cfg(growth_fn=fn)
+        arrs = _param_arrays(cfg)
+        arrs["sigma"][0, 3] = 0.0
+        p = _lib.Params(*[arrs[k].ctypes.data for k in ("WP", "WI", "WV", "K", "mu", "sigma", "M")])
+        rc = lib.slime_ca_check_params(ctypes.byref(cfg), ctypes.byref(p))
+        assert rc == (_lib.SLIME_OK if ok else _lib.SLIME_EINVAL), fn
 
 
 def test_check_params_rejects_null_and_invalid_config():

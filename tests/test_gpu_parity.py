@@ -203,6 +203,52 @@ def test_step_peaked_attention_matches_oracle(oracle, per_cell):
     np.testing.assert_allclose(mo, mi, rtol=1e-6)
 
 
+# ---- the growth functions and the per-cell conservation of the shipped kernel ----------------
+
+@pytest.mark.parametrize("dtype,D,fn,cons,per_cell", [
+    ("fp32", 64, 1, 0, False),
+    ("fp32", 64, 2, 1, True),
+    ("fp32", 16, 0, 1, False),
+    ("bf16", 64, 1, 0, False),   # matrix-core stencil with the general growth
+    ("bf16", 64, 2, 0, True),
+    ("bf16", 64, 0, 1, False),   # matrix-core stencil, per-cell conservation
+    ("bf16", 32, 1, 1, True),
+])
+def test_step_growth_and_conservation_variants_match_oracle(oracle, dtype, D, fn, cons, per_cell):
+    from tests.conftest import growth_variant_params
+    cfg = _cfg("variant", B=2, G=16, D=D, dtype=dtype, growth_per_cell=per_cell, pods=2)
+    X = make_state(cfg, seed=2)
+    if dtype == "bf16":
+        X = round_bf16(X)
+    p = growth_variant_params(cfg, oracle, X)
+    if dtype == "bf16":
+        p = {k: (round_bf16(v) if k in ("WP", "WI", "WV") else v) for k, v in p.items()}
+    with _engine(cfg, growth_fn=fn, conservation=cons) as e:
+        e.set_params(p)
+        x = _dev(X, dtype)
+        y1 = e.forward(x)
+        torch.cuda.synchronize()
+        mi, mo = e.mass()
+        y2 = e.forward(x, n_steps=2)
+        torch.cuda.synchronize()
+        mi2, mo2 = e.mass()
+        Y1, Y2 = _host(y1), _host(y2)
+    ocfg = _ocfg(cfg, growth_fn=fn, conservation=cons)
+    ref1, rmi, _ = oracle.step(ocfg, X, p, 1)
+    ref2, _, _ = oracle.step(ocfg, X, p, 2)
+    e1, e2 = norm_err(Y1, ref1), norm_err(Y2, ref2)
+    print(f"  growth_fn {fn}, conservation {cons}: 1 step {e1:.3e}, 2 steps {e2:.3e}")
+    assert e1 <= TOL[dtype] and e2 <= TOL[dtype]
+    np.testing.assert_allclose(mi, rmi, rtol=1e-6)
+    np.testing.assert_allclose(mo, mi, rtol=1e-6)
+    np.testing.assert_allclose(mo2, mi2, rtol=1e-6)
+    if cons == 1 and dtype == "fp32":
+        # every cell keeps its head sums (no cell of these states takes the guard)
+        cx = X.astype(np.float64).reshape(cfg.B, cfg.G, cfg.G, cfg.H, D).sum(-1)
+        cy = Y1.astype(np.float64).reshape(cfg.B, cfg.G, cfg.G, cfg.H, D).sum(-1)
+        np.testing.assert_allclose(cy, cx, rtol=1e-5, atol=1e-6 * np.abs(cx).max())
+
+
 # ---- full steps ------------------------------------------------------------------------------
 
 @pytest.mark.parametrize("dtype,per_cell,pods,chain,D", [
@@ -655,7 +701,18 @@ def test_neural_ca_update_matches_oracle_organism_sequence(oracle, D):
 
 # ---- full-size throughput shape: size-independent properties --------------------------------------
 
-def test_c3_shape_conserves_mass_and_matches_oracle_on_one_batch(oracle):
+C3_ENTRIES = [0, 21, 42, 63]  # batch entries of c3 compared with the oracle
+
+
+def _rms_err(got, ref) -> float:
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    return float(np.sqrt(np.mean((got - ref) ** 2)) / np.sqrt(np.mean(ref ** 2)))
+
+
+def test_c3_shape_conserves_mass_and_matches_oracle_on_four_batches(oracle):
+    # One step of the full c3 shape (64 x 128 x 128, bf16): four batch entries spread
+    # over the batch (and so over the stencil's tile tickets) against the oracle.
     from slime_amd import CONFIGS
     cfg = CONFIGS["c3"]
     p, X = _prep(cfg)
@@ -666,25 +723,55 @@ def test_c3_shape_conserves_mass_and_matches_oracle_on_one_batch(oracle):
         torch.cuda.synchronize()
         mi, mo = e.mass()
         assert bool(torch.isfinite(y.float()).all())
-        Y0 = _host(y[0:1])
+        Ys = _host(y[C3_ENTRIES])
     np.testing.assert_allclose(mo, mi, rtol=1e-6)
-    one = _ocfg(cfg, B=1)
-    ref, rmi, _ = oracle.step(one, X[0:1], p, 1)
-    err = norm_err(Y0, ref)
-    print(f"  batch 0 of c3: normalised error {err:.3e}")
-    assert err <= TOL["bf16"]
-    np.testing.assert_allclose(mi[0], rmi[0], rtol=1e-6)
+    sub = _ocfg(cfg, B=len(C3_ENTRIES))
+    ref, rmi, _ = oracle.step(sub, X[C3_ENTRIES], p, 1)
+    for j, b in enumerate(C3_ENTRIES):
+        err = norm_err(Ys[j], ref[j])
+        print(f"  batch {b} of c3: normalised error {err:.3e}")
+        assert err <= TOL["bf16"], b
+    np.testing.assert_allclose(mi[C3_ENTRIES], rmi, rtol=1e-6)
 
 
-def test_c3_bench_call_conserves_mass_and_repeats_bitwise():
-    # The benched call: 10 chained c3 steps in one slime_ca_step (each step's mass
-    # scale folded into the next step's weights and loads, the last step written in
-    # fp32 and rescaled once), run twice on one handle. At this size the checks are
-    # size-independent: every value finite, the stored state's per-(batch, head) sums
-    # equal the input's up to one bf16 rounding of each element, and the second call
-    # repeats the first bit for bit (the stencil's tile tickets decide which
-    # workgroup runs a tile, never what it computes). One step of batch 0 is
-    # compared with the oracle by the test above.
+def test_c3_two_step_call_matches_oracle_on_four_batches(oracle):
+    # The benched call's code path over two steps: step 2 reads step 1's unscaled
+    # bf16 output with its mass scale folded into the weights and the stencil's loads,
+    # the last step is written in fp32 and rescaled once into the bf16 state. Over
+    # two steps the oracle's own trajectory with bf16-rounded states stays within
+    # 1.0e-2 of its fp32 one, so the bf16 bar still measures the device there.
+    from slime_amd import CONFIGS
+    cfg = CONFIGS["c3"]
+    p, X = _prep(cfg)
+    with _engine(cfg) as e:
+        e.set_params(p)
+        y = e.forward(_dev(X, "bf16"), n_steps=2)
+        torch.cuda.synchronize()
+        mi, mo = e.mass()
+        Ys = _host(y[C3_ENTRIES])
+    np.testing.assert_allclose(mo, mi, rtol=1e-6)
+    ref, _, _ = oracle.step(_ocfg(cfg, B=len(C3_ENTRIES)), X[C3_ENTRIES], p, 2)
+    for j, b in enumerate(C3_ENTRIES):
+        err = norm_err(Ys[j], ref[j])
+        print(f"  batch {b} of c3 after 2 steps: normalised error {err:.3e}")
+        assert err <= TOL["bf16"], b
+
+
+def test_c3_bench_call_conserves_mass_repeats_bitwise_and_tracks_oracle(oracle):
+    """The benched call: 10 chained c3 steps in one slime_ca_step (each step's mass
+    scale folded into the next step's weights and loads, the last step written in
+    fp32 and rescaled once), run twice on one handle.
+
+    * every value finite; the stored state's per-(batch, head) sums equal the
+      input's up to one bf16 rounding of each element; the second call repeats the
+      first bit for bit (the stencil's tile tickets decide which workgroup runs a
+      tile, never what it computes);
+    * batch entry 0 against the oracle's 10 steps. The map is chaotic at bf16
+      resolution: the oracle's own trajectory with every state rounded to bf16 ends
+      2.9e-1 (max-normalised) from its fp32 trajectory after 10 steps, so a
+      max-norm bar there tests nothing. The RMS difference grows slowly (1.6e-3
+      after one step, 9.4e-3 after ten), and the device is held to 3x the RMS
+      difference of that bf16-state oracle trajectory, computed here."""
     from slime_amd import CONFIGS
     cfg = CONFIGS["c3"]
     p, X = _prep(cfg)
@@ -702,7 +789,19 @@ def test_c3_bench_call_conserves_mass_and_repeats_bitwise():
         assert bool(torch.isfinite(y1.float()).all())
         assert torch.equal(y1, y2)
         s_in, s_out = head_sums(x), head_sums(y1)
+        Y0 = _host(y1[0:1])
     np.testing.assert_allclose(mo, mi, rtol=1e-6)
     drift = np.abs(s_out - s_in) / np.abs(s_in)
     print(f"  10 chained c3 steps: max relative drift of the stored head sums {drift.max():.2e}")
     assert drift.max() <= 5e-5
+    one = _ocfg(cfg, B=1)
+    ref, cur = X[0:1], X[0:1]
+    for _ in range(10):
+        ref = oracle.step(one, ref, p, 1)[0]
+        cur = round_bf16(oracle.step(one, cur, p, 1)[0])
+    spread = _rms_err(cur, ref)
+    err = _rms_err(Y0, ref)
+    print(f"  batch 0 after 10 steps: RMS-normalised error {err:.3e} (max-normalised "
+          f"{norm_err(Y0, ref):.3e}); bf16-state oracle trajectory {spread:.3e} "
+          f"(max-normalised {norm_err(cur, ref):.3e})")
+    assert err <= 3.0 * spread

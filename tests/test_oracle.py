@@ -164,6 +164,73 @@ def test_growth_closed_forms(oracle):
     np.testing.assert_allclose(g1, 2 * math.exp(-z * z) - 1, atol=1e-5)
 
 
+def test_growth_gaussian_closed_forms(oracle):
+    """growth_fn 1, exp(-(U - mu)^2 / (2 sigma^2)) (failed_attempts/pseudopod.cu:46-48):
+    1 at mu, exp(-1/2) one sigma away on either side, exp(-2) at two sigma, and no
+    offset (the bell's 2 g - 1 would give 1, 0.213, -0.73 there)."""
+    cfg = OracleConfig(B=1, G=8, H=H, D=2, growth_fn=1)
+    mu = np.full((1, H), 0.2, np.float32)
+    sigma = np.full((1, H), 0.03, np.float32)
+
+    def g_at(u):
+        return oracle.growth(cfg, np.full((1, 8, 8, cfg.C), u, np.float32), mu, sigma)
+
+    np.testing.assert_allclose(g_at(0.2), 1.0, atol=1e-6)
+    np.testing.assert_allclose(g_at(0.23), math.exp(-0.5), rtol=1e-5)
+    np.testing.assert_allclose(g_at(0.17), math.exp(-0.5), rtol=1e-5)
+    np.testing.assert_allclose(g_at(0.26), math.exp(-2.0), rtol=1e-5)
+    np.testing.assert_allclose(g_at(5.0), 0.0, atol=1e-30)
+
+
+def test_growth_shipped_closed_forms(oracle):
+    """growth_fn 2, the shipped kernel's U exp(-U^2) (slime/core/pseudopod.cu:183):
+    odd, zero at 0, +-1/e at +-1, its maximum exp(-1/2)/sqrt(2) at 1/sqrt(2); mu and
+    sigma play no part."""
+    cfg = OracleConfig(B=1, G=8, H=H, D=2, growth_fn=2)
+    r = _rng(13)
+    mu = r.uniform(0.1, 0.3, (1, H)).astype(np.float32)
+    sigma = r.uniform(0.01, 0.05, (1, H)).astype(np.float32)
+
+    def g_at(u):
+        return oracle.growth(cfg, np.full((1, 8, 8, cfg.C), u, np.float32), mu, sigma)
+
+    np.testing.assert_allclose(g_at(0.0), 0.0, atol=1e-30)
+    np.testing.assert_allclose(g_at(1.0), math.exp(-1.0), rtol=1e-6)
+    np.testing.assert_allclose(g_at(-1.0), -math.exp(-1.0), rtol=1e-6)
+    np.testing.assert_allclose(g_at(2 ** -0.5), math.exp(-0.5) * 2 ** -0.5, rtol=1e-6)
+    U = r.normal(0, 1, (1, 8, 8, cfg.C)).astype(np.float32)
+    np.testing.assert_allclose(oracle.growth(cfg, -U, mu, sigma), -oracle.growth(cfg, U, mu, sigma),
+                               rtol=1e-6)
+    for u in (0.6, 0.7, 0.75, 0.9):  # 1/sqrt(2) = 0.7071 is the maximum
+        assert g_at(u).max() <= math.exp(-0.5) * 2 ** -0.5 + 1e-7
+
+
+@pytest.mark.parametrize("D,per_cell", [(64, False), (16, True)])
+def test_growth_variant_case_tells_the_functions_apart(oracle, D, per_cell):
+    """On the inputs of the GPU growth-variant cases (tests.conftest.
+    growth_variant_params), one step with each growth function differs from the
+    others by more than 5x the bf16 bar, and a Gaussian with sigma^2 in place of
+    2 sigma^2 by more than 3x, so a device computing the wrong function fails those
+    cases."""
+    from slime_amd import make_state
+    from slime_amd.synthetic import CAConfig
+    from tests.conftest import growth_variant_params
+    scfg = CAConfig("variant", B=2, G=16, H=H, D=D, dtype="fp32", steps=1, w_std=0.05, pods=2,
+                    growth_per_cell=per_cell)
+    X = make_state(scfg, seed=2)
+    p = growth_variant_params(scfg, oracle, X)
+    Ys = {fn: oracle.step(OracleConfig(B=2, G=16, H=H, D=D, pods=2, growth_per_cell=per_cell,
+                                       growth_fn=fn), X, p, 1)[0] for fn in (0, 1, 2)}
+    for a, b in ((0, 1), (0, 2), (1, 2)):
+        moved = norm_err(Ys[a], Ys[b])
+        print(f"  growth {a} vs {b}: {moved:.3f}")
+        assert moved > 5 * 2e-2, (a, b)
+    q = dict(p, sigma=(p["sigma"] / np.sqrt(2.0)).astype(np.float32))  # exp(-(U-mu)^2 / sigma^2)
+    wrong = oracle.step(OracleConfig(B=2, G=16, H=H, D=D, pods=2, growth_per_cell=per_cell,
+                                     growth_fn=1), X, q, 1)[0]
+    assert norm_err(wrong, Ys[1]) > 3 * 2e-2
+
+
 def test_growth_per_cell_parameters(oracle):
     cfg = OracleConfig(B=1, G=8, H=H, D=2, growth_per_cell=True)
     r = _rng(11)
@@ -293,6 +360,39 @@ def test_mix_closed_forms(oracle):
 
 # ---- S7 conservation ------------------------------------------------------------------------
 
+def test_conserve_per_cell_sums_and_guard(oracle):
+    """conservation 1, the shipped per-(cell, head) renormalisation
+    (slime/core/pseudopod.cu:160-165,196-203): every cell's head sum of Y equals
+    that of X; a cell whose head sum of Y is within the 1e-6 guard keeps its values;
+    the per-(b, head) totals are then conserved as well."""
+    cfg = OracleConfig(B=2, G=8, H=H, D=4, conservation=1)
+    r = _rng(17)
+    X = r.random((2, 8, 8, cfg.C), dtype=np.float32)
+    Y = (X * r.uniform(0.5, 1.5, X.shape)).astype(np.float32)
+    Y[1, 3, 4, 2 * 4:3 * 4] = np.array([1e-7, -1e-7, 2e-7, 0.0], np.float32)  # guard cell
+    Yc, mi, mo = oracle.conserve(cfg, X, Y)
+    sx = X.astype(np.float64).reshape(2, 8, 8, H, 4).sum(-1)
+    sy = Yc.astype(np.float64).reshape(2, 8, 8, H, 4).sum(-1)
+    other = np.ones(sx.shape, bool)
+    other[1, :, :, 2] = False
+    np.testing.assert_allclose(sy[other], sx[other], rtol=1e-6)
+    # batch 1, head 2 holds the guard cell: its mass is missing from the head total
+    # after the per-cell pass, and the global pass puts it back by one factor over
+    # the head, so every other cell of that head keeps one common ratio
+    ratio = sy[1, :, :, 2] / sx[1, :, :, 2]
+    ratio = np.delete(ratio.reshape(-1), 3 * 8 + 4)
+    np.testing.assert_allclose(ratio, ratio[0], rtol=1e-6)
+    assert ratio[0] > 1.0 + 1e-4
+    np.testing.assert_allclose(mo, mi, rtol=1e-12)
+    # a state that already matches X cell by cell is left as it is
+    Yi, _, _ = oracle.conserve(cfg, X, X)
+    np.testing.assert_allclose(Yi, X, rtol=1e-6)
+    # against the global-only mode the cells differ, the totals agree
+    Yg, _, mo0 = oracle.conserve(OracleConfig(B=2, G=8, H=H, D=4), X, Y)
+    assert norm_err(Yg, Yc) > 1e-2
+    np.testing.assert_allclose(mo0, mo, rtol=1e-12)
+
+
 def test_conserve_sums_and_guard(oracle):
     cfg = OracleConfig(B=2, G=8, H=H, D=4)
     X, Y = _state(cfg), _state(cfg, 8) * 3.0
@@ -340,9 +440,17 @@ def _numpy_step(cfg, X, p):
             mu, sg = p["mu"][q][..., None], p["sigma"][q][..., None]
         else:
             mu, sg = p["mu"][q][None, None, :, None], p["sigma"][q][None, None, :, None]
-        g = 2 * np.exp(-((U - mu) / (sg + 1e-7)) ** 2) - 1
+        if cfg.growth_fn == 1:
+            g = np.exp(-(U - mu) ** 2 / (2 * sg.astype(np.float64) ** 2))
+        elif cfg.growth_fn == 2:
+            g = U * np.exp(-U * U)
+        else:
+            g = 2 * np.exp(-((U - mu) / (sg + 1e-7)) ** 2) - 1
         Z = xh + cfg.dt * g * Vt
         Y = np.einsum("oh,yxhc->yxoc", p["M"][q].astype(np.float64), Z)
+        if cfg.conservation == 1:
+            cx, cy = xh.sum(axis=3, keepdims=True), Y.sum(axis=3, keepdims=True)
+            Y = Y * np.where(np.abs(cy) > 1e-6, cx / np.where(cy == 0, 1, cy), 1.0)
         sx = xh.sum(axis=(0, 1, 3))
         sy = Y.sum(axis=(0, 1, 3))
         scale = np.where(np.abs(sy) > 1e-6, sx / sy, 1.0)
@@ -350,9 +458,11 @@ def _numpy_step(cfg, X, p):
     return out
 
 
-@pytest.mark.parametrize("per_cell,pods", [(False, 1), (True, 2)])
-def test_step_matches_numpy_restatement(oracle, per_cell, pods):
-    cfg = OracleConfig(B=2, G=8, H=H, D=8, pods=pods, growth_per_cell=per_cell)
+@pytest.mark.parametrize("per_cell,pods,fn,cons", [(False, 1, 0, 0), (True, 2, 0, 0), (False, 2, 1, 0),
+                                                   (True, 1, 2, 1), (False, 1, 0, 1)])
+def test_step_matches_numpy_restatement(oracle, per_cell, pods, fn, cons):
+    cfg = OracleConfig(B=2, G=8, H=H, D=8, pods=pods, growth_per_cell=per_cell, growth_fn=fn,
+                       conservation=cons)
     p, X = _params(cfg, w_std=0.1), _state(cfg)
     Y, mi, mo = oracle.step(cfg, X, p, 1)
     ref = _numpy_step(cfg, X, p)
