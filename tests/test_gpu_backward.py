@@ -31,8 +31,12 @@ def _cfg(B, G, D, dtype, **kw):
     return CAConfig("bw", B=B, G=G, H=8, D=D, dtype=dtype, steps=1, w_std=0.05, **kw)
 
 
-def _inputs(cfg, seed=1):
-    p = make_params(cfg, seed=seed)
+def _inputs(cfg, seed=1, peaked=False):
+    if peaked:  # peaked attention: the S4 backward carries a large share of the gradients
+        from tests.conftest import peaked_params
+        p = peaked_params(cfg, seed=seed)
+    else:
+        p = make_params(cfg, seed=seed)
     X = make_state(cfg, seed=seed + 1)
     T = np.random.default_rng(seed + 2).random(X.shape, dtype=np.float32)
     if cfg.dtype == "bf16":
@@ -46,23 +50,26 @@ def _dev(a, dtype):
     return t.to(torch.bfloat16 if dtype == "bf16" else torch.float32).contiguous()
 
 
-@pytest.mark.parametrize("dtype,D,pods,per_cell,B,G", [
-    ("fp32", 16, 2, False, 2, 16),
-    ("fp32", 32, 1, True, 2, 16),
-    ("bf16", 64, 1, False, 2, 16),
-    ("bf16", 64, 2, True, 2, 16),
+@pytest.mark.parametrize("dtype,D,pods,per_cell,B,G,peaked", [
+    # the peaked-attention weights of tests.conftest.peaked_params
+    ("bf16", 64, 2, False, 2, 16, True),
+    ("fp32", 64, 1, True, 2, 16, True),
+    ("fp32", 16, 2, False, 2, 16, False),
+    ("fp32", 32, 1, True, 2, 16, False),
+    ("bf16", 64, 1, False, 2, 16, False),
+    ("bf16", 64, 2, True, 2, 16, False),
     # C = 256: one wave per cell in the cell pass, one 256-column tile per operand in dW
-    ("bf16", 32, 2, False, 2, 16),
+    ("bf16", 32, 2, False, 2, 16, False),
     # C = 128: the 128 x 128 weight-gradient tiles
-    ("bf16", 16, 1, True, 2, 16),
+    ("bf16", 16, 1, True, 2, 16, False),
     # the smallest grid: 64 cells per pod, fewer than 8 whole cell-pass iterations
-    ("fp32", 8, 1, False, 1, 8),
-    ("fp32", 8, 3, True, 3, 8),
+    ("fp32", 8, 1, False, 1, 8, False),
+    ("fp32", 8, 3, True, 3, 8, False),
 ])
-def test_backward_matches_oracle(oracle, dtype, D, pods, per_cell, B, G):
+def test_backward_matches_oracle(oracle, dtype, D, pods, per_cell, B, G, peaked):
     cfg = _cfg(B=B, G=G, D=D, dtype=dtype, pods=pods, growth_per_cell=per_cell)
-    print(f"[case] backward {dtype} D={D} pods={pods} per_cell={per_cell}", flush=True)
-    p, X, T = _inputs(cfg)
+    print(f"[case] backward {dtype} D={D} pods={pods} per_cell={per_cell} peaked={peaked}", flush=True)
+    p, X, T = _inputs(cfg, peaked=peaked)
     with Pseudopod(cfg.B, cfg.G, cfg.H, cfg.D, cfg.dtype, cfg.dt, per_cell, pods) as e:
         e.set_params(p)
         loss, gx, grads = e.backward(_dev(X, dtype), _dev(T, dtype))
