@@ -147,10 +147,18 @@ def _trace_work(workload: str) -> dict:
 
 
 def _short_name(full: str) -> str:
+    """The kernel's name and template arguments, without namespaces or parameters."""
     name = full.replace("void ", "", 1)
     for pre in ("slime::(anonymous namespace)::", "slime::"):
         name = name.replace(pre, "")
     return name.split("(")[0].strip()
+
+
+def _work_key(name: str) -> str:
+    """The name with the boolean template arguments of a kernel's variants removed
+    (the growth-function instantiations do the same work per launch)."""
+    import re
+    return re.sub(r", (true|false)", "", name)
 
 
 def trace_summary(path: str, workload: str, cells: int = 1 << 20) -> str:
@@ -169,9 +177,9 @@ def trace_summary(path: str, workload: str, cells: int = 1 << 20) -> str:
              "work per launch | achieved | of peak |",
              "|---|---|---|---|---|---|---|---|---|---|---|"]
     for name, calls, avg, tot, pct, mn, mx in sorted(rows, key=lambda r: -r[3]):
-        if name not in work:
+        if _work_key(name) not in work:
             continue
-        what, kind, per_cell = work[name]
+        what, kind, per_cell = work[_work_key(name)]
         cols = [f"`{name}`", what, str(calls), f"{avg / 1e3:.1f}", f"{mn / 1e3:.1f}", f"{mx / 1e3:.1f}",
                 f"{tot / 1e6:.2f}", f"{pct:.2f}"]
         if kind == "B":
