@@ -131,7 +131,7 @@ def _trace_work(workload: str) -> dict:
         }
     if workload == "c5":
         return {
-            "bw_cell_kernel<unsigned short, 64>": (
+            "bw_cell_ring_kernel": (
                 "S7-S4 per (cell, head), tape for the gathers", "B",
                 5 * C * 2 + C * 4 + 3 * C * 4 + C * 2 + 2 * 8 * 9 * 4),
             "bw_gather_tile_kernel<unsigned short>": (

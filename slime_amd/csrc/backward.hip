@@ -468,6 +468,309 @@ void bw_cell_kernel(BackwardArgs a) {
     }
 }
 
+// ---- the cell pass for bf16, D = 64: neighbours staged in an LDS ring along each row ----------
+// The same per-(cell, head) sums as bw_cell_kernel, in the same order, for the c5 shape.
+// Instead of 27 loads per lane from L2 per iteration (three planes, nine neighbours),
+// a workgroup walks whole rows of cells, two cells per iteration, and keeps the
+// neighbourhood columns of X, I and V (three rows, eight heads, 9 KiB per column) in a
+// ring of six column slots: the two columns of the next iteration are staged by direct
+// global->LDS loads while the current one computes, so each column crosses L2 once per
+// row instead of once per neighbour, and its latency is hidden. The tape stores of an
+// iteration are issued after the next iteration's barrier (their values wait in
+// registers), so the wait for the staged columns at an iteration's start does not wait
+// for the stores just issued.
+namespace ring {
+constexpr int kSlots = 6;                          // column slots (prefetch distance 1)
+constexpr int kRowB = 128;                         // one (cell, head) row, bf16 D = 64
+constexpr int kColB = 3 * 3 * kHeads * kRowB;      // [plane X, I, V][dy][head] rows: 9 KiB
+constexpr int kInstPerCol = kColB / 1024;          // direct-load instructions per column (9)
+
+__device__ __forceinline__ unsigned lds_addr(const void* p) {
+    return (unsigned)(size_t)(const __attribute__((address_space(3))) void*)p;
+}
+__device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
+// 16 bytes per lane from base + voff to LDS byte address lds + 16 * lane
+// (global_load_lds_dwordx4, SGPR base, 32-bit lane offset; waited for by wait_vm0).
+// The base and the LDS address are uniform; readfirstlane makes that visible to the
+// register allocator (both operands must be SGPRs).
+__device__ __forceinline__ void dma16(const void* base, unsigned voff, unsigned lds) {
+    asm volatile(
+        "s_mov_b32 m0, %0\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, %2"
+        :
+        : "s"(lds), "v"(voff), "s"(base)
+        : "memory", "m0");
+}
+}  // namespace ring
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+void bw_cell_ring_kernel(BackwardArgs a) {
+    using T = bf16_t;
+    constexpr int kD = 64, H = kHeads, C = H * kD, kL = kD / 4, kCpi = 256 / kL / H;  // 2 cells
+    __shared__ __attribute__((aligned(16))) unsigned char sring[ring::kSlots * ring::kColB];
+    __shared__ __attribute__((aligned(16))) float sgy[kCpi * C];  // gY of the iteration's cells
+    __shared__ float skw[H * 9], smc[H * H];
+    __shared__ float red[kPartF][256];
+    const int G = a.G;
+    const long long cells = (long long)G * G;
+    const int pod = blockIdx.x / a.nW;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int grp = tid / kL, li = tid % kL;
+    const int cs = __builtin_amdgcn_readfirstlane(grp / H), h = grp % H;  // a wave holds one cell
+    const int c0 = 4 * li;
+    if (tid < H * 9) skw[tid] = a.K[pod * H * 9 + tid];
+    else if (tid < H * 9 + H * H) {
+        const int j = tid - H * 9, hh = j / H, o = j % H;  // smc[hh * H + o] = M[o][hh]
+        smc[j] = a.M[(pod * H + o) * H + hh];
+    }
+#pragma unroll
+    for (int q = 0; q < kPartF; ++q) red[q][tid] = 0.f;
+    const float* kw = skw + h * 9;
+    const float* mcol = smc + h * H;
+    const float inv_sqrt_d = 1.0f / __builtin_sqrtf((float)kD);
+    const float dt = a.dt;
+    // Rows of the pod: XCD x (workgroups are dealt to the XCDs in turn) walks the x-th
+    // eighth of them, its workgroups on adjacent rows, whose staged rows overlap in its L2.
+    const int rows_pod = a.per_pod * G;
+    const bool banded = rows_pod % 8 == 0 && a.nW % 8 == 0;
+    const int nWx = banded ? a.nW / 8 : a.nW;
+    const int wx = banded ? (blockIdx.x % a.nW) / 8 : blockIdx.x % a.nW;
+    const int band = banded ? rows_pod / 8 : rows_pod;
+    const int band0 = banded ? (blockIdx.x % 8) * band : 0;
+    const unsigned sbase = ring::lds_addr(sring);
+    const unsigned char* sr = sring;
+    // tape values of the previous iteration, stored after the next iteration's barrier
+    float t_gu[4], t_gvt[4], t_gpt[4], t_gxd[4], t_a = 0.f, t_gs = 0.f;
+    long long t_ir = -1, t_r = 0;
+    auto store_tape = [&]() {
+        if (t_ir < 0) return;
+        st4f(a.gU, t_ir, t_gu);
+        st4f(a.gVt, t_ir, t_gvt);
+        st4<T>(a.G3, t_r * 3 * C + h * kD + c0, t_gpt);
+        st4f(a.gXd, t_ir, t_gxd);
+        if (li < 9) {
+            a.att[(t_r * H + h) * 9 + li] = t_a;
+            a.gS[(t_r * H + h) * 9 + li] = t_gs;
+        }
+    };
+
+    for (int row = wx; row < band; row += nWx) {
+        __syncthreads();  // LDS set up; the previous row's last iteration is done with its slots
+        const int rr = band0 + row;                      // row of the pod
+        const int b = pod * a.per_pod + rr / G, y = rr % G;
+        const long long bb = (long long)b * cells * C * 2;  // bytes to batch entry b
+        const char* srcX = reinterpret_cast<const char*>(a.X) + bb;
+        const char* srcI = reinterpret_cast<const char*>(a.I) + bb;
+        const char* srcV = reinterpret_cast<const char*>(a.V) + bb;
+        // Stage column positions p0 .. p0 + kNp - 1 (position p is column p - 1, wrapped):
+        // instruction j of a column covers plane j / 3, dy = j % 3, the eight heads (8
+        // lanes of 16 bytes each); wave w issues instructions w, w + 4, ...
+        const unsigned lane_off = (unsigned)(((lane >> 3) * kD + (lane & 7) * 8) * 2);
+        const int yrow[3] = {wrapb(y - 1, G), y, wrapb(y + 1, G)};
+        auto stage = [&](auto np_c, int p0) {
+            constexpr int kNp = decltype(np_c)::value;
+#pragma unroll
+            for (int q = 0; q < kNp * ring::kInstPerCol; ++q) {
+                if (q % 4 != wave) continue;
+                const int p = p0 + q / ring::kInstPerCol, j = q % ring::kInstPerCol;
+                const int pl = j / 3, dy = j % 3;
+                const int col = wrapb(p - 1, G);
+                const unsigned voff = (unsigned)(((long long)yrow[dy] * G + col) * C * 2) + lane_off;
+                const char* src = pl == 0 ? srcX : (pl == 1 ? srcI : srcV);
+                ring::dma16(src, voff, sbase + (p % ring::kSlots) * ring::kColB + j * 1024);
+            }
+        };
+        stage(std::integral_constant<int, 4>{}, 0);  // the first iteration's four columns
+        // The centre values of a cell (P, Y, T; mu and sigma when per cell) are loaded
+        // one iteration ahead, into registers; the row's (batch, head) factors once.
+        const long long row_r = (long long)b * cells + (long long)y * G;
+        auto centre_pi = [&](int x) { return ((long long)pod * cells + (long long)y * G + x) * H + h; };
+        Raw4<T> n_p = ldraw4<T>(a.P, (row_r + cs) * C + h * kD + c0);
+        Raw4<T> n_t = ldraw4<T>(a.T, (row_r + cs) * C + h * kD + c0);
+        F4 n_y = ld4f(a.Y, (row_r + cs) * C + h * kD + c0);
+        float n_mu = 0.f, n_sg = 0.f;
+        if (a.per_cell) {
+            n_mu = a.mu[centre_pi(cs)];
+            n_sg = a.sigma[centre_pi(cs)];
+        }
+        const float rs = a.scale[b * H + h], rsl = a.scale[a.B * H + b * H + h];
+        const float cy = a.coef[(b * H + h) * 3 + 0], cq = a.coef[(b * H + h) * 3 + 1],
+                    cyl = a.coef[(b * H + h) * 3 + 2];
+        const float pod_mu = a.mu[pod * H + h], pod_sg = a.sigma[pod * H + h];
+        for (int i = 0; i < G / 2; ++i) {
+            const int x0 = 2 * i;
+            ring::wait_vm0();  // this wave's staging of the iteration's columns has landed
+            __syncthreads();   // ... and every wave's; iteration i - 1 is done with its slots
+            const Raw4<T> p_raw = n_p, t_raw = n_t;
+            const F4 yv = n_y;
+            const float mu = a.per_cell ? n_mu : pod_mu, sg = a.per_cell ? n_sg : pod_sg;
+            store_tape();
+            if (i + 1 < G / 2) {
+                stage(std::integral_constant<int, 2>{}, x0 + 4);  // the next iteration's two new columns
+                const long long in = (row_r + x0 + 2 + cs) * C + h * kD + c0;
+                n_p = ldraw4<T>(a.P, in);
+                n_t = ldraw4<T>(a.T, in);
+                n_y = ld4f(a.Y, in);
+                if (a.per_cell) {
+                    n_mu = a.mu[centre_pi(x0 + 2 + cs)];
+                    n_sg = a.sigma[centre_pi(x0 + 2 + cs)];
+                }
+            }
+            const int x = x0 + cs;
+            const long long r = row_r + x;
+            const long long ir = r * C + h * kD + c0;
+            // ---- forward locals of head h at r (4 channels) ----
+            Raw4<T> xk[9], ik[9], vk[9];
+#pragma unroll
+            for (int k = 0; k < 9; ++k) {
+                const int dy = k / 3, dx = k % 3;  // neighbour (y + dy - 1, x + dx - 1)
+                const unsigned char* base =
+                    sr + ((x + dx) % ring::kSlots) * ring::kColB + (dy * H + h) * ring::kRowB + c0 * 2;
+                xk[k] = *reinterpret_cast<const Raw4<T>*>(base);
+                ik[k] = *reinterpret_cast<const Raw4<T>*>(base + 3 * H * ring::kRowB);
+                vk[k] = *reinterpret_cast<const Raw4<T>*>(base + 6 * H * ring::kRowB);
+            }
+            const F4 pc{{raw_at<T>(p_raw, 0), raw_at<T>(p_raw, 1), raw_at<T>(p_raw, 2), raw_at<T>(p_raw, 3)}};
+            const F4 tv{{raw_at<T>(t_raw, 0), raw_at<T>(t_raw, 1), raw_at<T>(t_raw, 2), raw_at<T>(t_raw, 3)}};
+            const float inv_sp = 1.0f / (sg + 1e-7f);
+            float t[4], et[4], g[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float u = 0.f;
+#pragma unroll
+                for (int k = 0; k < 9; ++k) u = __builtin_fmaf(kw[k], raw_at<T>(xk[k], e), u);
+                t[e] = (u - mu) * inv_sp;
+                et[e] = __expf(-t[e] * t[e]);
+                g[e] = 2.0f * et[e] - 1.0f;
+            }
+            float s[9], mx = -3.0e38f;
+#pragma unroll
+            for (int k = 0; k < 9; ++k) {
+                float d = 0.f;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) d = __builtin_fmaf(pc.v[e], raw_at<T>(ik[k], e), d);
+                s[k] = lanes_sum<kL>(d) * inv_sqrt_d;
+                mx = fmaxf(mx, s[k]);
+            }
+            float den = 0.f;
+#pragma unroll
+            for (int k = 0; k < 9; ++k) {
+                s[k] = __expf(s[k] - mx);
+                den += s[k];
+            }
+            const float rden = 1.0f / den;
+            float vt[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int k = 0; k < 9; ++k) {
+                s[k] *= rden;  // a_k
+#pragma unroll
+                for (int e = 0; e < 4; ++e) vt[e] = __builtin_fmaf(s[k], raw_at<T>(vk[k], e), vt[e]);
+            }
+            float z[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) z[e] = __builtin_fmaf(dt * g[e], vt[e], raw_at<T>(xk[4], e));
+            // ---- S7 -> gY of output head h at (r, c0..c0+3), shared; S6 -> gZ_h ----
+            {
+                float gyo[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float u = 2.0f * (__builtin_fmaf(rs, yv.v[e], rsl * yv.v[e]) - tv.v[e]) * a.inv_n - cq;
+                    gyo[e] = __builtin_fmaf(cy, u, cyl * u);
+                }
+                *reinterpret_cast<float4*>(sgy + cs * C + h * kD + c0) = make_float4(gyo[0], gyo[1], gyo[2], gyo[3]);
+            }
+            __syncthreads();  // the next iteration's first barrier orders sgy's next writes
+            float gz[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int o = 0; o < H; ++o) {
+                const float4 gq = *reinterpret_cast<const float4*>(sgy + cs * C + o * kD + c0);
+                const float gy[4] = {gq.x, gq.y, gq.z, gq.w};
+                const float mo = mcol[o];
+                float pm = red[o][tid];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    gz[e] = __builtin_fmaf(mo, gy[e], gz[e]);
+                    pm = __builtin_fmaf(gy[e], z[e], pm);
+                }
+                red[o][tid] = pm;
+            }
+            // ---- S6, S3 ----
+            float gu[4], gvt[4], gmu_l = 0.f, gsg_l = 0.f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float gg = dt * gz[e] * vt[e];
+                gvt[e] = dt * gz[e] * g[e];
+                gu[e] = gg * (-4.0f * t[e] * et[e]) * inv_sp;
+                gmu_l -= gu[e];
+                gsg_l -= gu[e] * t[e];
+            }
+            if (a.per_cell) {
+                const float smu = lanes_sum<kL>(gmu_l), ssg = lanes_sum<kL>(gsg_l);
+                if (li == 0) {
+                    a.gcell[(r * H + h) * 2 + 0] = smu;
+                    a.gcell[(r * H + h) * 2 + 1] = ssg;
+                }
+            } else {
+                red[H + 9][tid] += gmu_l;
+                red[H + 10][tid] += gsg_l;
+            }
+#pragma unroll
+            for (int k = 0; k < 9; ++k) {
+                float pk = red[H + k][tid];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) pk = __builtin_fmaf(gu[e], raw_at<T>(xk[k], e), pk);
+                red[H + k][tid] = pk;
+            }
+            // ---- S5, S4 ----
+            float ga[9], sa = 0.f;
+#pragma unroll
+            for (int k = 0; k < 9; ++k) {
+                float d = 0.f;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) d = __builtin_fmaf(gvt[e], raw_at<T>(vk[k], e), d);
+                ga[k] = lanes_sum<kL>(d);
+                sa = __builtin_fmaf(s[k], ga[k], sa);
+            }
+            float gp[4] = {0.f, 0.f, 0.f, 0.f};
+            float tape_a = 0.f, tape_gs = 0.f;  // lane li < 9 holds a_li and gs_li
+#pragma unroll
+            for (int k = 0; k < 9; ++k) {
+                const float gs = s[k] * (ga[k] - sa);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) gp[e] = __builtin_fmaf(gs * inv_sqrt_d, raw_at<T>(ik[k], e), gp[e]);
+                tape_a = k == li ? s[k] : tape_a;
+                tape_gs = k == li ? gs : tape_gs;
+            }
+            // the tape waits in registers until the next iteration's barrier
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                t_gu[e] = gu[e];
+                t_gvt[e] = gvt[e];
+                t_gpt[e] = pc.v[e] > 0.f ? gp[e] : 0.f;
+                t_gxd[e] = gz[e] + cq;
+            }
+            t_a = tape_a;
+            t_gs = tape_gs;
+            t_ir = ir;
+            t_r = r;
+        }
+    }
+    __syncthreads();
+    store_tape();
+    // block reduction of the parameter partials, fixed order: per head h, the threads of
+    // groups g = cs * H + h, in the order (cs, lane)
+    if (tid < H * kPartF) {
+        const int hh = tid / kPartF, q = tid % kPartF;
+        float sum = 0.f;
+        for (int c2 = 0; c2 < kCpi; ++c2)
+#pragma unroll
+            for (int l2 = 0; l2 < kL; ++l2) sum += red[q][(c2 * H + hh) * kL + l2];
+        a.ppart[((long long)(pod * H + hh) * a.nW + blockIdx.x % a.nW) * kPartF + q] = sum;
+    }
+}
+
 // ---- gathers: gV, gI~ (planes 2 and 1 of G3) and the potential's transpose -------------------
 // One lane per 4 channels of one (cell q, head): cell q collects from the 9 cells
 // r = q - offset_k whose neighbour k it is.
@@ -1006,7 +1309,10 @@ hipError_t launch_dt(const BackwardArgs& a, hipStream_t s) {
     const long long n = (long long)a.B * cells * kHeads * kD;
     hipLaunchKernelGGL((bw_loss_partial_kernel<T>), dim3(a.lchunks, a.B), dim3(256), 0, s, a);
     hipLaunchKernelGGL(bw_loss_finalize_kernel, dim3(a.B * kHeads), dim3(256), 0, s, a);
-    hipLaunchKernelGGL((bw_cell_kernel<T, kD>), dim3(a.pods * a.nW), dim3(256), 0, s, a);
+    if constexpr (sizeof(T) == 2 && kD == 64)  // G is a multiple of 8: whole cell pairs per row
+        hipLaunchKernelGGL(bw_cell_ring_kernel, dim3(a.pods * a.nW), dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL((bw_cell_kernel<T, kD>), dim3(a.pods * a.nW), dim3(256), 0, s, a);
     if constexpr (kD == 64)
         hipLaunchKernelGGL((bw_gather_tile_kernel<T>),
                            dim3((unsigned)(a.B * (cells / (kGTy * kGTx)) * kHeads)), dim3(256), 0, s, a);
