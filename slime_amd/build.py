@@ -21,7 +21,7 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libslime_ca.so")
 PROBE_LIB = os.path.join(HERE, "libslime_probe.so")  # measured ceilings (calibrate.py)
-SOURCES = ["api.cpp", "gemm.hip", "gemm_add.hip", "stencil.hip", "mass.hip", "fitness.hip", "organism.hip",
+SOURCES = ["api.cpp", "gemm.hip", "gemm_add.hip", "gemm_tape.hip", "stencil.hip", "mass.hip", "fitness.hip", "organism.hip",
            "backward.hip", "pool.hip"]
 ARCH = "gfx950"
 

@@ -226,8 +226,9 @@ class DeviceScope {
 
 // S1 for one step: per-batch weights (scaled by the deferred mass scale of x),
 // then the projection GEMM(s).
+// With `pre` (parallel projections only), I before its GELU is also written there.
 int run_project(slime_ca* h, const void* x, const float* x_scale, void* P, void* I, void* V,
-                hipStream_t s) {
+                hipStream_t s, void* pre = nullptr) {
     const slime_ca_config& c = h->cfg;
     const int C = h->C;
     WeightPrepArgs w{};
@@ -258,8 +259,20 @@ int run_project(slime_ca* h, const void* x, const float* x_scale, void* P, void*
         g.act[0] = 1;
         g.act[1] = 2;
         g.act[2] = 0;
-        HIP_TRY(timed(h, h->gemm_ev, s, [&] { return launch_gemm(c.dtype, g, s); }));
+        if (pre && gemm_uses_mfma(c.dtype, g)) {
+            HIP_TRY(timed(h, h->gemm_ev, s, [&] { return launch_gemm_tape(c.dtype, g, pre, s); }));
+        } else {
+            HIP_TRY(timed(h, h->gemm_ev, s, [&] { return launch_gemm(c.dtype, g, s); }));
+            if (pre) {  // I before its GELU: the W_I plane again, identity
+                g.Bt = static_cast<const char*>(h->Wt) + (size_t)C * C * h->elem;
+                g.N = C;
+                g.out[0] = pre;
+                g.act[0] = 0;
+                HIP_TRY(launch_gemm(c.dtype, g, s));
+            }
+        }
     } else {
+        if (pre) return fail(SLIME_EINVAL, "the pre-activation output needs parallel projections");
         // pvi_chain 2: P reads the 3x3 neighbourhood sum of x, held in V until V's own
         // product overwrites it. The deferred mass scale of x is per (b, head), so it
         // scales the neighbourhood sum as it scales x, and plane 0 still carries it.
@@ -863,23 +876,9 @@ int slime_ca_backward(slime_ca* h, const void* x_in, const void* target, float* 
     hipStream_t s = static_cast<hipStream_t>(stream);
     h->last_stream = s;
 
-    // forward tape: P, I, V; I before its GELU; the unscaled fp32 output and the scale
-    rc = run_project(h, x_in, nullptr, h->P, h->I, h->V, s);
+    // forward tape: P, I, V and I before its GELU; the unscaled fp32 output and the scale
+    rc = run_project(h, x_in, nullptr, h->P, h->I, h->V, s, h->Ipre);
     if (rc) return rc;
-    {
-        GemmArgs g{};
-        g.A = x_in;
-        g.Bt = static_cast<const char*>(h->Wt) + C * C * h->elem;  // plane I of the per-batch weights
-        g.bt_batch_stride = 3LL * C * C;
-        g.rows_per_batch = c.G * c.G;
-        g.M = c.B * c.G * c.G;
-        g.N = (int)C;
-        g.K = (int)C;
-        g.out[0] = h->Ipre;
-        g.ncol = (int)C;
-        g.act[0] = 0;
-        HIP_TRY(launch_gemm(c.dtype, g, s));
-    }
     float* y32 = h->Sf ? h->Sf : h->bw_y32;
     float* rs = h->scale[0];
     rc = run_stencil(h, x_in, nullptr, h->P, h->I, h->V, y32, 1, rs, s);

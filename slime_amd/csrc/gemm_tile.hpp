@@ -1,8 +1,10 @@
 // gemm_tile.hpp — the MFMA tile kernel of the [P|I|V] projections (gemm.hip), kept in
-// a header so that a second translation unit (gemm_add.hip) can build, with
-// SLIME_GEMM_ADD defined, its backward variant: one fp32 output plane written as the
-// product plus an addend (dL/dX = the direct part + the part through the
-// projections). Without the macro this is exactly the forward kernel.
+// a header so that other translation units can build its backward variants:
+// gemm_add.hip with SLIME_GEMM_ADD (one fp32 output plane written as the product plus
+// an addend: dL/dX = the direct part + the part through the projections) and
+// gemm_tape.hip with SLIME_GEMM_TAPE (the forward projections, the GELU plane also
+// written before its activation, for the backward's tape). Without either macro this
+// is exactly the forward kernel.
 #pragma once
 
 #include <type_traits>
@@ -368,11 +370,55 @@ __device__ __forceinline__ void store_tile_bf16(f32x16 (&acc)[4][4], char* ob, i
     store_group<7>(ob, gl, ncol, t[1]);
 }
 
+#ifdef SLIME_GEMM_TAPE
+// The identity epilogue of a tile whose accumulators stay live afterwards (the tape
+// kernel's pre-activation plane): each group (32 rows x 64 columns: accumulator
+// blocks [2p][j] and [2p+1][j] of group 2j+p) is converted just before it is staged,
+// so one group's bf16 values are held at a time rather than the whole tile's, and
+// the pass needs no registers the accumulators would otherwise free. The stores are
+// those of store_tile_bf16<0>: same bytes, same places.
+template <int Gr>
+__device__ __forceinline__ void convert_group_identity(f32x16 (&acc)[4][4], uint2 (&v)[8]) {
+    constexpr int j = Gr / 2, p = Gr % 2;
+    pin_acc(acc[2 * p][j]);
+    pin_acc(acc[2 * p + 1][j]);
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            v[4 * ii + q] = make_uint2(pack_bf16x2(acc[2 * p + ii][j][4 * q + 0], acc[2 * p + ii][j][4 * q + 1]),
+                                       pack_bf16x2(acc[2 * p + ii][j][4 * q + 2], acc[2 * p + ii][j][4 * q + 3]));
+}
+__device__ __forceinline__ void stage_write_group(const uint2 (&v)[8], unsigned char* epi, unsigned w_off) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) *reinterpret_cast<uint2*>(epi + epi_w_piece(w_off, k)) = v[k];
+}
+__device__ __forceinline__ void store_tile_bf16_identity_lean(f32x16 (&acc)[4][4], char* ob, int ncol,
+                                                              unsigned char* epi, unsigned ep_w,
+                                                              const unsigned char* ep_r, unsigned gl) {
+    uint2 v[2][8];
+    uint4 t[2][4];
+    convert_group_identity<0>(acc, v[0]);
+    stage_write_group(v[0], epi, ep_w);
+    stage_read(ep_r, t[0]);
+    static_for<1, 8>([&](auto gc) {
+        constexpr int Gr = decltype(gc)::value;
+        convert_group_identity<Gr>(acc, v[Gr & 1]);
+        stage_write_group(v[Gr & 1], epi, ep_w);
+        stage_read(ep_r, t[Gr & 1]);
+        store_group<Gr - 1>(ob, gl, ncol, t[(Gr - 1) & 1]);
+    });
+    store_group<7>(ob, gl, ncol, t[1]);
+}
+#endif
+
 template <typename T>
-#ifndef SLIME_GEMM_ADD
-__global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs g) {
-#else
+#if defined(SLIME_GEMM_ADD)
 __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_add_kernel(GemmArgs g, const float* add) {
+#elif defined(SLIME_GEMM_TAPE)
+__global__ __launch_bounds__(kThreads, 1) void gemm_mfma_tape_kernel(GemmArgs g, void* pre) {
+#else
+__global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs g) {
 #endif
     __shared__ __attribute__((aligned(1024))) unsigned char lds[4 * kStageB];
     constexpr bool kBf16 = sizeof(T) == 2;
@@ -429,7 +475,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_add_kernel(GemmArgs g, 
         if (wk.next >= 0) tile_rows<T>(g, wk.next, wk.nN, &wk.x_nxt, &wk.w_nxt);
         else wk.x_nxt = wk.x_cur, wk.w_nxt = wk.w_cur;
         // Loads younger than slab kt+1 when step kt waits for it: slabs kt+2 and
-        // kt+3, and for kt <= 2 after an epilogue also that epilogue's stores.
+        // kt+3, and for kt <= 2 after an epilogue also that epilogue's stores (after
+        // the tape variant's two epilogues of a GELU tile, more than are counted:
+        // the wait then also covers some of those stores).
         constexpr int y_store = kStores + 2 * kDmaPerSlab <= 63 ? kStores + 2 * kDmaPerSlab : 0;
         const int y_first = stores_pending ? y_store : 2 * kDmaPerSlab;
         if (wk.nk == 4) {
@@ -451,6 +499,20 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_add_kernel(GemmArgs g, 
             const long long off = wave_el + f32_lane_elem(lane, g.ncol);
             store_tile_f32_add(acc, static_cast<float*>(g.out[plane]) + off, add + off, g.ncol);
         } else
+#endif
+#ifdef SLIME_GEMM_TAPE
+        if (g.act[plane] == 2) {  // the GELU plane also leaves before its activation
+            asm volatile("; epilogue pre-activation");
+            if constexpr (kBf16)
+                store_tile_bf16_identity_lean(acc, reinterpret_cast<char*>(reinterpret_cast<bf16_t*>(pre) + wave_el),
+                                              g.ncol, epi, ep_w, ep_r, ep_gl);
+            else
+                store_tile_f32<0>(acc, static_cast<float*>(pre) + wave_el + f32_lane_elem(lane, g.ncol), g.ncol);
+            // Ordered after every store above (memory clobber) and before the second
+            // epilogue's accumulator pins (volatile): the two conversions do not
+            // overlap, so each holds the registers of one.
+            asm volatile("; epilogue pre-activation done" ::: "memory");
+        }
 #endif
         if constexpr (kBf16) {
             char* obase = reinterpret_cast<char*>(reinterpret_cast<bf16_t*>(out) + wave_el);

@@ -31,6 +31,9 @@ hipError_t launch_gemm(int dtype, const GemmArgs& a, hipStream_t s);
 // One output plane (N = ncol, identity) written as fp32 out[0] = A Bt^T + add, add of
 // out[0]'s layout (in place allowed); MFMA shapes only (else hipErrorInvalidValue).
 hipError_t launch_gemm_add_f32(int dtype, const GemmArgs& a, const float* add, hipStream_t s);
+// As launch_gemm, and every output plane with the GELU activation is also written
+// before it to `pre` (that plane's layout); MFMA shapes only (else hipErrorInvalidValue).
+hipError_t launch_gemm_tape(int dtype, const GemmArgs& a, void* pre, hipStream_t s);
 
 // The perception input of the reference's S1 (pvi_chain = 2): S = the toroidal 3x3
 // neighbourhood sum of every channel of X, [B][G][G][C] in the storage type
