@@ -117,7 +117,12 @@ def cpu_baseline(cfg, params, X, seconds: float):
 # ---- rocprofv3 kernel-trace summaries ------------------------------------------------
 # Algorithmic work per launch of the kernels of each workload: ("B", bytes) for an
 # HBM-bound kernel, ("F", flops) for a matrix-core one, per cell of the launch
-# (1,048,576 cells in c3 and c5). Reads and writes are counted once per cell.
+# (_TRACE_CELLS: 1,048,576 cells in c3 and c5, 16 pods x 128 x 128 = 262,144 in c4).
+# Reads and writes are counted once per cell.
+_TRACE_CELLS = {"c3": 1 << 20, "c5": 1 << 20, "c4": 16 * 128 * 128}
+
+
+
 def _trace_work(workload: str) -> dict:
     C = 512
     if workload == "c3":
@@ -138,10 +143,24 @@ def _trace_work(workload: str) -> dict:
                 "gV, gI~, potential transpose", "B", 3 * C * 4 + 2 * C * 2 + 2 * 8 * 9 * 4 + 2 * C * 2 + C * 4),
             "gemm_mfma_add_kernel<unsigned short>": ("dX GEMM + direct part", "F", 2 * C * 3 * C),
             "bw_dw_mfma2_kernel": ("weight gradients", "F", 2 * C * 3 * C),
-            "gemm_mfma_kernel<unsigned short>": ("tape projections, I before GELU, forward", None, None),
+            "gemm_mfma_tape_kernel<unsigned short>": ("tape projections, I also before GELU", "F", 2 * C * 3 * C),
+            "gemm_mfma_kernel<unsigned short>": ("forward projections (the forward timing)", None, None),
             "stencil_mfma_kernel<float>": ("tape step, fp32 out", "B", 4 * C * 2 + C * 4),
             "stencil_mfma_kernel<unsigned short>": ("forward step", "B", 5 * C * 2),
             "bw_loss_partial_kernel<unsigned short>": ("loss partials", "B", C * 4 + C * 2),
+        }
+    if workload == "c4":
+        return {
+            "fitness_finalize_kernel<64>": ("Jacobi eigenvalues, effective rank, fitness", None, None),
+            "gemm_mfma_kernel<unsigned short>": ("[P\\|I\\|V] projection GEMM", "F", 2 * C * 3 * C),
+            "stencil_mfma_kernel<float>": ("single-step calls: fp32 out", "B", 4 * C * 2 + C * 4),
+            "fitness_partial_kernel<unsigned short, 64>": (
+                "8-state history read once, fp64 Gram of the last", "B", 8 * C * 2),
+            "stencil_mfma_kernel<unsigned short>": ("rollout: bf16 states", "B", 5 * C * 2),
+            "rescale_kernel<float, unsigned short>": ("single-step calls only", "B", C * 4 + C * 2),
+            "weight_prep_kernel<unsigned short>": ("per-pod scaled weights", None, None),
+            "mass_finalize_kernel": ("S7 factors", None, None),
+            "fill_f64_kernel": ("the rollout's unit factors of state 0", None, None),
         }
     return {}
 
@@ -161,12 +180,14 @@ def _work_key(name: str) -> str:
     return re.sub(r", (true|false)", "", name)
 
 
-def trace_summary(path: str, workload: str, cells: int = 1 << 20) -> str:
+def trace_summary(path: str, workload: str, cells: int = 0) -> str:
     """Markdown table of a rocprofv3 --stats kernel CSV: calls and durations of each
     kernel and, for the kernels of `workload` with a known algorithmic work, the
-    achieved rate and its fraction of the MI355X peak."""
+    achieved rate and its fraction of the MI355X peak (`cells` per launch: the
+    workload's own when 0)."""
     import csv
     work = _trace_work(workload)
+    cells = cells or _TRACE_CELLS.get(workload, 1 << 20)
     rows = []
     with open(path) as f:
         for r in csv.DictReader(f):
@@ -197,6 +218,59 @@ def trace_summary(path: str, workload: str, cells: int = 1 << 20) -> str:
     return "\n".join(lines)
 
 
+# ---- rocprofv3 --pmc HBM traffic summaries ------------------------------------------
+# The kernels whose traffic bench.py reports, keyed as pmc_traffic.json keys them, with
+# the short names of their workload's launches.
+_TRAFFIC_KERNELS = {"c3": {"stencil": "stencil_mfma_kernel<unsigned short, false>",
+                           "gemm": "gemm_mfma_kernel<unsigned short>"}}
+
+
+def _counter_means(run_dir: str, counter: str) -> dict:
+    """Mean per dispatch of `counter` (KiB as rocprofv3 reads it) by kernel short name,
+    with the number of dispatches, from <run_dir>/run_counter_collection.csv."""
+    import csv
+    import collections
+    sums, disp = collections.defaultdict(float), collections.defaultdict(set)
+    with open(os.path.join(run_dir, "run_counter_collection.csv")) as f:
+        for r in csv.DictReader(f):
+            if r["Counter_Name"] != counter:
+                continue
+            k = _short_name(r["Kernel_Name"])
+            sums[k] += float(r["Counter_Value"])
+            disp[k].add(r["Dispatch_Id"])
+    return {k: (sums[k] / len(disp[k]), len(disp[k])) for k in sums}
+
+
+def traffic_summary(root: str, workload: str = "c3") -> tuple:
+    """HBM bytes per launch from four rocprofv3 --pmc runs under `root`: p_FETCH_SIZE and
+    p_WRITE_SIZE over the bench command, pc_FETCH_SIZE and pc_WRITE_SIZE over the 1 GiB
+    copy of `python3 -m slime_amd.calibrate --mib 1024`. Each counter is scaled by what
+    it reads for that copy (1 GiB read, 1 GiB written). Returns (markdown, json dict)."""
+    fetch = _counter_means(os.path.join(root, "p_FETCH_SIZE"), "FETCH_SIZE")
+    write = _counter_means(os.path.join(root, "p_WRITE_SIZE"), "WRITE_SIZE")
+    cf = _counter_means(os.path.join(root, "pc_FETCH_SIZE"), "FETCH_SIZE")["__amd_rocclr_copyBuffer"]
+    cw = _counter_means(os.path.join(root, "pc_WRITE_SIZE"), "WRITE_SIZE")["__amd_rocclr_copyBuffer"]
+    kib = 1 << 20  # the copy moves 1 GiB each way
+    f_fac, w_fac = kib / cf[0], kib / cw[0]
+    lines = [f"Calibration: the 1 GiB copy reads FETCH_SIZE = {cf[0]:,.0f} KiB (mean of {cf[1]} "
+             f"dispatches) and WRITE_SIZE = {cw[0]:,.0f} KiB, so HBM bytes = FETCH_SIZE × "
+             f"{f_fac:.4f} × 1024 and WRITE_SIZE × {w_fac:.4f} × 1024.", "",
+             "| kernel | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | read GB | write GB | total GB |",
+             "|---|---|---|---|---|---|---|"]
+    out = {}
+    names = {v: k for k, v in _TRAFFIC_KERNELS.get(workload, {}).items()}
+    for k in sorted(fetch, key=lambda n: -fetch[n][0]):
+        if k not in write:
+            continue
+        rd, wr = fetch[k][0] * f_fac * 1024, write[k][0] * w_fac * 1024
+        lines.append(f"| `{k}` | {fetch[k][1]} | {fetch[k][0]:,.0f} | {write[k][0]:,.0f} | "
+                     f"{rd / 1e9:.3f} | {wr / 1e9:.3f} | {(rd + wr) / 1e9:.3f} |")
+        if k in names:
+            out[names[k]] = {"read_bytes": round(rd), "write_bytes": round(wr),
+                             "bytes_per_launch": round(rd + wr)}
+    return "\n".join(lines), {workload: out}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -211,10 +285,20 @@ def main() -> int:
                     help="time the c4 ensemble: 16 pods' steps and the fused fitness")
     ap.add_argument("--trace-summary", metavar="CSV",
                     help="print a markdown roofline table of a rocprofv3 kernel_stats.csv "
-                         "(no GPU needed) for --config c3 or c5, then exit")
+                         "(no GPU needed) for --config c3, c4 or c5, then exit")
+    ap.add_argument("--traffic-summary", metavar="DIR",
+                    help="print the HBM bytes per launch from the four rocprofv3 --pmc runs "
+                         "under DIR (p_FETCH_SIZE, p_WRITE_SIZE, pc_FETCH_SIZE, pc_WRITE_SIZE; "
+                         "no GPU needed) as markdown and pmc_traffic.json's JSON, then exit")
     args = ap.parse_args()
     if args.trace_summary:
         print(trace_summary(args.trace_summary, args.config))
+        return 0
+    if args.traffic_summary:
+        md, js = traffic_summary(args.traffic_summary, args.config)
+        print(md)
+        print()
+        print(json.dumps(js, indent=1))
         return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported in this "
