@@ -1239,29 +1239,53 @@ __global__ __launch_bounds__(256) void bw_dw_mfma2_kernel(BackwardArgs a, DwArgs
     for (int kb = 0; kb < 8; ++kb)
 #pragma unroll
         for (int jb = 0; jb < 8; ++jb) acc[kb][jb] = f32x4{0.f, 0.f, 0.f, 0.f};
-    if (nsteps > 0) {
-#pragma unroll
-        for (int st = 0; st < kDw2Stages - 1; ++st) issue(st, st);
-    }
-    for (int st = 0; st < nsteps; ++st) {
-        dw_wait<8 * (kDw2Stages - 2)>();  // this wave's loads of step st have landed
-        dw_barrier();                     // ... and every wave's; step st-1's stage is free
-        issue(st + kDw2Stages - 1, (st + kDw2Stages - 1) % kDw2Stages);
+    // The fragments of step st + 1 are read while step st's MFMAs run (from registers),
+    // so the matrix cores do not wait for each step's LDS reads: one wave per SIMD
+    // has no other wave to cover them. A stage is refilled once every wave has read
+    // its fragments (the barrier of the step after).
+    auto read_frags = [&](int st, uint4 (&A)[8], uint4 (&Bv)[8]) {
         const unsigned char* base = lds + (st % kDw2Stages) * kDw2StageB;
-        uint4 av[8], bv[8];
 #pragma unroll
         for (int b = 0; b < 8; ++b) {
             const uint2 x0 = dw_tr16(base + roff[0][b][0]), x1 = dw_tr16(base + roff[0][b][1]);
             const uint2 g0 = dw_tr16(base + roff[1][b][0]), g1 = dw_tr16(base + roff[1][b][1]);
-            av[b] = make_uint4(x0.x, x0.y, x1.x, x1.y);
-            bv[b] = make_uint4(g0.x, g0.y, g1.x, g1.y);
+            A[b] = make_uint4(x0.x, x0.y, x1.x, x1.y);
+            Bv[b] = make_uint4(g0.x, g0.y, g1.x, g1.y);
         }
+    };
+    uint4 av[8], bv[8];
+    if (nsteps > 0) {
 #pragma unroll
-        for (int kb = 0; kb < 8; ++kb)
+        for (int st = 0; st < kDw2Stages; ++st) issue(st, st);
+        dw_wait<8 * (kDw2Stages - 1)>();  // this wave's loads of step 0 have landed
+        dw_barrier();                     // ... and every wave's
+        read_frags(0, av, bv);
+    }
+    for (int st = 0; st < nsteps; ++st) {
+        dw_wait<8 * (kDw2Stages - 2)>();  // this wave's loads of step st + 1 have landed
+        dw_barrier();                     // ... and every wave's; step st's stage is read
+        issue(st + kDw2Stages, st % kDw2Stages);
+        // each row of 8 MFMAs is followed by the reads of one block of step st + 1's
+        // fragments (past the last step: the refetched last step, unused)
+        const unsigned char* nbase = lds + ((st + 1) % kDw2Stages) * kDw2StageB;
+        uint4 an[8], bn[8];
+#pragma unroll
+        for (int kb = 0; kb < 8; ++kb) {
 #pragma unroll
             for (int jb = 0; jb < 8; ++jb)
                 acc[kb][jb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
                     __builtin_bit_cast(bf16x8_v, av[kb]), __builtin_bit_cast(bf16x8_v, bv[jb]), acc[kb][jb], 0, 0, 0);
+            const uint2 x0 = dw_tr16(nbase + roff[0][kb][0]), x1 = dw_tr16(nbase + roff[0][kb][1]);
+            const uint2 g0 = dw_tr16(nbase + roff[1][kb][0]), g1 = dw_tr16(nbase + roff[1][kb][1]);
+            an[kb] = make_uint4(x0.x, x0.y, x1.x, x1.y);
+            bn[kb] = make_uint4(g0.x, g0.y, g1.x, g1.y);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            av[b] = an[b];
+            bv[b] = bn[b];
+        }
     }
     dw_wait<0>();  // refetched steps may still be landing in LDS
     float* out = d.part + (long long)chunk * C * N3;
