@@ -65,6 +65,9 @@ def _dev(a, dtype):
     # the smallest grid: 64 cells per pod, fewer than 8 whole cell-pass iterations
     ("fp32", 8, 1, False, 1, 8, False),
     ("fp32", 8, 3, True, 3, 8, False),
+    # bf16, D = 64 on the smallest grid: the LDS-ring cell pass with rows of 8 cells (4
+    # iterations, every column slot reused), per-cell growth, two pods of one entry each
+    ("bf16", 64, 2, True, 2, 8, True),
 ])
 def test_backward_matches_oracle(oracle, dtype, D, pods, per_cell, B, G, peaked):
     cfg = _cfg(B=B, G=G, D=D, dtype=dtype, pods=pods, growth_per_cell=per_cell)
