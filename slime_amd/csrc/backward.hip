@@ -484,24 +484,6 @@ constexpr int kSlots = 6;                          // column slots (prefetch dis
 constexpr int kRowB = 128;                         // one (cell, head) row, bf16 D = 64
 constexpr int kColB = 3 * 3 * kHeads * kRowB;      // [plane X, I, V][dy][head] rows: 9 KiB
 constexpr int kInstPerCol = kColB / 1024;          // direct-load instructions per column (9)
-
-__device__ __forceinline__ unsigned lds_addr(const void* p) {
-    return (unsigned)(size_t)(const __attribute__((address_space(3))) void*)p;
-}
-__device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
-// 16 bytes per lane from base + voff to LDS byte address lds + 16 * lane
-// (global_load_lds_dwordx4, SGPR base, 32-bit lane offset; waited for by wait_vm0).
-// The base and the LDS address are uniform; readfirstlane makes that visible to the
-// register allocator (both operands must be SGPRs).
-__device__ __forceinline__ void dma16(const void* base, unsigned voff, unsigned lds) {
-    asm volatile(
-        "s_mov_b32 m0, %0\n\t"
-        "s_nop 0\n\t"
-        "global_load_lds_dwordx4 %1, %2"
-        :
-        : "s"(lds), "v"(voff), "s"(base)
-        : "memory", "m0");
-}
 }  // namespace ring
 
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
@@ -539,7 +521,7 @@ void bw_cell_ring_kernel(BackwardArgs a) {
     const int wx = banded ? (blockIdx.x % a.nW) / 8 : blockIdx.x % a.nW;
     const int band = banded ? rows_pod / 8 : rows_pod;
     const int band0 = banded ? (blockIdx.x % 8) * band : 0;
-    const unsigned sbase = ring::lds_addr(sring);
+    const unsigned sbase = lds_addr(sring);
     const unsigned char* sr = sring;
     // tape values of the previous iteration, stored after the next iteration's barrier
     float t_gu[4], t_gvt[4], t_gpt[4], t_gxd[4], t_a = 0.f, t_gs = 0.f;
@@ -579,7 +561,7 @@ void bw_cell_ring_kernel(BackwardArgs a) {
                 const int col = wrapb(p - 1, G);
                 const unsigned voff = (unsigned)(((long long)yrow[dy] * G + col) * C * 2) + lane_off;
                 const char* src = pl == 0 ? srcX : (pl == 1 ? srcI : srcV);
-                ring::dma16(src, voff, sbase + (p % ring::kSlots) * ring::kColB + j * 1024);
+                dma16_lds(src, voff, sbase + (p % ring::kSlots) * ring::kColB + j * 1024);
             }
         };
         stage(std::integral_constant<int, 4>{}, 0);  // the first iteration's four columns
@@ -601,7 +583,7 @@ void bw_cell_ring_kernel(BackwardArgs a) {
         const float pod_mu = a.mu[pod * H + h], pod_sg = a.sigma[pod * H + h];
         for (int i = 0; i < G / 2; ++i) {
             const int x0 = 2 * i;
-            ring::wait_vm0();  // this wave's staging of the iteration's columns has landed
+            wait_vm0();  // this wave's staging of the iteration's columns has landed
             __syncthreads();   // ... and every wave's; iteration i - 1 is done with its slots
             const Raw4<T> p_raw = n_p, t_raw = n_t;
             const F4 yv = n_y;
@@ -1060,7 +1042,6 @@ constexpr long long kDwRowsMfma = 16384;
 
 typedef short dw_v4i16 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) dw_v4i16 dw_lds_v4i16;
-typedef __attribute__((address_space(3))) void dw_lds_void;
 
 __device__ __forceinline__ uint2 dw_tr16(const unsigned char* p) {
     const dw_v4i16 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -1068,18 +1049,8 @@ __device__ __forceinline__ uint2 dw_tr16(const unsigned char* p) {
     return __builtin_bit_cast(uint2, v);
 }
 
-// One direct global->LDS load (global_load_lds_dwordx4, SGPR base + 32-bit lane
-// offset): lane l's 16 bytes land at LDS byte address lds + 16 l. The ring waits
-// for these loads itself (dw_wait) before the barrier that publishes a stage.
-__device__ __forceinline__ void dw_dma16(const void* base, unsigned voff, unsigned lds) {
-    asm volatile(
-        "s_mov_b32 m0, %0\n\t"
-        "s_nop 0\n\t"
-        "global_load_lds_dwordx4 %1, %2"
-        :
-        : "s"(lds), "v"(voff), "s"(base)
-        : "memory", "m0");
-}
+// The ring's direct loads (dma16_lds, common.hpp) are waited for by dw_wait before the
+// barrier that publishes a stage.
 template <int N>
 __device__ __forceinline__ void dw_wait() {
     __builtin_amdgcn_s_waitcnt((N & 15) | (((N >> 4) & 3) << 14) | 0x0F70);
@@ -1112,12 +1083,12 @@ __global__ __launch_bounds__(256) void bw_dw_mfma_kernel(BackwardArgs a, DwArgs 
     const unsigned xoff = (unsigned)(drow * C * 2 + dchunk * 16), goff = (unsigned)(drow * N3 * 2 + dchunk * 16);
     auto issue = [&](int st, int stage) {  // step st (clamped: past the end refetch the last)
         const long long rb = (long long)(st < nsteps ? st : nsteps - 1) * kDwStep;
-        const unsigned sb = (unsigned)(size_t)(const dw_lds_void*)(lds + stage * kDwStageB);
+        const unsigned sb = lds_addr(lds + stage * kDwStageB);
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             const int q = 2 * wave + u;
-            dw_dma16(Xs + (rb + 4 * q) * C * 2, xoff, sb + q * 1024);
-            dw_dma16(Gs + (rb + 4 * q) * N3 * 2, goff, sb + kDwStep * kDwRowB + q * 1024);
+            dma16_lds(Xs + (rb + 4 * q) * C * 2, xoff, sb + q * 1024);
+            dma16_lds(Gs + (rb + 4 * q) * N3 * 2, goff, sb + kDwStep * kDwRowB + q * 1024);
         }
     };
     // operand reads: 16-lane group g covers rows 8 g .. 8 g + 7 of a step (two reads)
@@ -1209,14 +1180,14 @@ __global__ __launch_bounds__(256) void bw_dw_mfma2_kernel(BackwardArgs a, DwArgs
     const unsigned xoff = (unsigned)(drow * C * 2 + dchunk * 16), goff = (unsigned)(drow * N3 * 2 + dchunk * 16);
     auto issue = [&](int st, int stage) {  // step st (clamped: past the end refetch the last)
         const long long rb = (long long)(st < nsteps ? st : nsteps - 1) * kDwStep;
-        const unsigned sb = (unsigned)(size_t)(const dw_lds_void*)(lds + stage * kDw2StageB);
+        const unsigned sb = lds_addr(lds + stage * kDw2StageB);
 #pragma unroll
         for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
                 const int q = 2 * wave + u;
-                dw_dma16(Xs + (rb + 4 * q) * C * 2 + sub * kDwRowB, xoff, sb + sub * kDw2SubB + q * 1024);
-                dw_dma16(Gs + (rb + 4 * q) * N3 * 2 + sub * kDwRowB, goff, sb + (2 + sub) * kDw2SubB + q * 1024);
+                dma16_lds(Xs + (rb + 4 * q) * C * 2 + sub * kDwRowB, xoff, sb + sub * kDw2SubB + q * 1024);
+                dma16_lds(Gs + (rb + 4 * q) * N3 * 2 + sub * kDwRowB, goff, sb + (2 + sub) * kDw2SubB + q * 1024);
             }
     };
     // operand reads: as in bw_dw_mfma_kernel (16-lane group g reads rows 8 g .. 8 g + 7)

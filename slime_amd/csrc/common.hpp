@@ -123,6 +123,46 @@ __device__ __forceinline__ float group_sum_n(float v) {
     return v;
 }
 
+// ---- direct global->LDS loads -------------------------------------------------
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// LDS byte address of a __shared__ object.
+__device__ __forceinline__ unsigned lds_addr(const void* p) {
+    return (unsigned)(size_t)(const lds_void_t*)p;
+}
+
+// s_waitcnt vmcnt(0): this wave's vector-memory operations, direct loads included,
+// have completed.
+__device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// One direct global->LDS load (global_load_lds_dwordx4 with an SGPR base and a 32-bit
+// lane offset): 16 bytes per lane from base + voff land at LDS byte address
+// lds + 16 * lane. Issued through inline asm, so that the per-lane addresses stay
+// 32-bit and the compiler does not make every later LDS read wait for all such loads
+// in flight (it cannot tell which buffer they fill): each kernel waits for them
+// itself (vmcnt) before the barrier that publishes them. base and lds are uniform.
+__device__ __forceinline__ void dma16_lds(const void* base, unsigned voff, unsigned lds) {
+    asm volatile(
+        "s_mov_b32 m0, %0\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, %2"
+        :
+        : "s"(lds), "v"(voff), "s"(base)
+        : "memory", "m0");
+}
+
+// As dma16_lds, with the nontemporal hint: for rows read once, so that they do not
+// displace from L2 the lines that neighbouring workgroups share.
+__device__ __forceinline__ void dma16_lds_nt(const void* base, unsigned voff, unsigned lds) {
+    asm volatile(
+        "s_mov_b32 m0, %0\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, %2 nt"
+        :
+        : "s"(lds), "v"(voff), "s"(base)
+        : "memory", "m0");
+}
+
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float rcp_fast(float x) { return __builtin_amdgcn_rcpf(x); }
 

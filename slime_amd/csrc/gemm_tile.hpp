@@ -85,27 +85,8 @@ __device__ __forceinline__ void store_tile_f32_add(f32x16 (&acc)[4][4], float* o
 }
 #endif
 
-typedef __attribute__((address_space(3))) void lds_void_t;
-
-// One direct global->LDS load (global_load_lds_dwordx4, SGPR base + 32-bit lane
-// offset): 16 bytes per lane from base + voff land at LDS byte address
-// lds_base + 16 * lane. Issued through inline asm: the compiler would otherwise
-// make every later LDS read wait for all such loads still in flight (it cannot
-// tell which stage they fill). The pipeline waits for each slab itself (wait_vm)
-// before the barrier that publishes it.
-__device__ __forceinline__ void dma16(const void* base, unsigned voff, unsigned lds_base) {
-    asm volatile(
-        "s_mov_b32 m0, %0\n\t"
-        "s_nop 0\n\t"
-        "global_load_lds_dwordx4 %1, %2"
-        :
-        : "s"(lds_base), "v"(voff), "s"(base)
-        : "memory", "m0");
-}
-
-__device__ __forceinline__ unsigned lds_addr(const void* p) {
-    return (unsigned)(size_t)(const lds_void_t*)p;
-}
+// Direct global->LDS loads: dma16_lds (common.hpp). The pipeline waits for each slab
+// itself (wait_vm) before the barrier that publishes it.
 
 // Issues the direct global->LDS loads of slab ks of a tile into the stage at LDS
 // byte address sbase: 32 instructions of 16 rows each; wave w issues row groups
@@ -116,9 +97,9 @@ __device__ __forceinline__ void issue_slab(const char* x, const char* w, long lo
                                            int wave, unsigned voff, unsigned sbase) {
     const long long k_off = dma_k_off(ks);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) dma16(x + dma_grp_off(j, wave, row_bytes) + k_off, voff, sbase + dma_lds_off(j, wave));
+    for (int j = 0; j < 4; ++j) dma16_lds(x + dma_grp_off(j, wave, row_bytes) + k_off, voff, sbase + dma_lds_off(j, wave));
 #pragma unroll
-    for (int j = 4; j < 8; ++j) dma16(w + dma_grp_off(j, wave, row_bytes) + k_off, voff, sbase + dma_lds_off(j, wave));
+    for (int j = 4; j < 8; ++j) dma16_lds(w + dma_grp_off(j, wave, row_bytes) + k_off, voff, sbase + dma_lds_off(j, wave));
 }
 
 // s_waitcnt vmcnt(n) for the counts the pipeline needs (immediate operand).
@@ -259,7 +240,7 @@ __device__ __forceinline__ void slab_step(const Walk& wk, int kt, int wave, unsi
     static_for<0, kDmaPerSlab>([&](auto jj) {
         constexpr int j = decltype(jj)::value;
         __builtin_amdgcn_sched_barrier(0);
-        dma16((j < 4 ? xs : ws) + dma_grp_off(j, wave, wk.row_bytes) + k_off, wk.voff, sb + dma_lds_off(j, wave));
+        dma16_lds((j < 4 ? xs : ws) + dma_grp_off(j, wave, wk.row_bytes) + k_off, wk.voff, sb + dma_lds_off(j, wave));
         if constexpr (kReadNext) read_frag<j>(f, rd, fb);
         mfma_group<T, false, 16 + 2 * j>(acc, f);
         mfma_group<T, false, 17 + 2 * j>(acc, f);

@@ -77,44 +77,8 @@ struct Layout {
                          offP = 3 * kHaloPad * kRowB;
 };
 
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(1))) const void gbl_void_t;
-
-__device__ __forceinline__ void wait_vm0() {
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // s_waitcnt vmcnt(0)
-}
-
-__device__ __forceinline__ unsigned lds_addr(const void* p) {
-    return (unsigned)(size_t)(const lds_void_t*)p;
-}
-
-// One direct global->LDS load (global_load_lds_dwordx4, SGPR base + 32-bit lane
-// offset): 16 bytes per lane from base + voff land at LDS byte address
-// lds + 16 * lane. Issued through inline asm so that the per-lane addresses stay
-// 32-bit (no 64-bit pointer per load held across the head loop); the kernel
-// waits for these loads itself (wait_vm0) before the barrier that publishes them.
-__device__ __forceinline__ void dma16_saddr(const void* base, unsigned voff, unsigned lds) {
-    asm volatile(
-        "s_mov_b32 m0, %0\n\t"
-        "s_nop 0\n\t"
-        "global_load_lds_dwordx4 %1, %2"
-        :
-        : "s"(lds), "v"(voff), "s"(base)
-        : "memory", "m0");
-}
-
-// As dma16_saddr, with the nontemporal hint: for rows read once (the tile's centre P),
-// so that they do not displace from L2 the halo lines neighbouring tiles share. Cuts
-// the stencil's L2 fetches by ~3.5 %.
-__device__ __forceinline__ void dma16_saddr_nt(const void* base, unsigned voff, unsigned lds) {
-    asm volatile(
-        "s_mov_b32 m0, %0\n\t"
-        "s_nop 0\n\t"
-        "global_load_lds_dwordx4 %1, %2 nt"
-        :
-        : "s"(lds), "v"(voff), "s"(base)
-        : "memory", "m0");
-}
+// Direct global->LDS loads: dma16_lds, dma16_lds_nt, wait_vm0 (common.hpp); the kernel
+// waits for them (wait_vm0) before the barrier that publishes them.
 
 // Workgroup barrier for LDS data only. __syncthreads() also waits for every
 // outstanding vector-memory operation (its release fence covers the direct
@@ -283,13 +247,13 @@ __global__ __launch_bounds__((Layout<T, D>::kThreads), 2) void stencil_kernel(St
 #pragma unroll
         for (int k = 0; k < L::kIA; ++k) {
             const unsigned row = lds_addr(buf) + (wave + k * L::kWaves) * 1024;
-            dma16_saddr(srcX, boff_lin[k] + hb, row + L::offX);
-            dma16_saddr(srcV, boff_lin[k] + hb, row + L::offV);
-            dma16_saddr(srcI, boff_swz[k] + hb, row + L::offI);
+            dma16_lds(srcX, boff_lin[k] + hb, row + L::offX);
+            dma16_lds(srcV, boff_lin[k] + hb, row + L::offV);
+            dma16_lds(srcI, boff_swz[k] + hb, row + L::offI);
         }
 #pragma unroll
         for (int k = 0; k < L::kPA; ++k)
-            dma16_saddr(srcP, boff_p[k] + hb, lds_addr(buf) + L::offP + (wave + k * L::kWaves) * 1024);
+            dma16_lds(srcP, boff_p[k] + hb, lds_addr(buf) + L::offP + (wave + k * L::kWaves) * 1024);
     };
 
     // Per-head parameters (and per-cell growth parameters) go to LDS once, before
@@ -707,11 +671,11 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
             const unsigned row = lb + (wave + 4 * k) * 1024;
-            dma16_saddr(srcX, boff_xv[k] + hb, row + offX);
-            dma16_saddr(srcV, boff_xv[k] + hb, row + offV);
-            dma16_saddr(srcI, boff_i[k] + hb, row + offI);
+            dma16_lds(srcX, boff_xv[k] + hb, row + offX);
+            dma16_lds(srcV, boff_xv[k] + hb, row + offV);
+            dma16_lds(srcI, boff_i[k] + hb, row + offI);
         }
-        dma16_saddr_nt(srcP, boff_p + hb, lb + offP + wave * 1024);
+        dma16_lds_nt(srcP, boff_p + hb, lb + offP + wave * 1024);
     };
     // Per-tile parameters: up to four values per lane, loaded into registers with
     // the tile's first staging and written to LDS once they have landed.
