@@ -145,7 +145,7 @@ def _trace_work(workload: str) -> dict:
             "bw_dw_mfma2_kernel": ("weight gradients", "F", 2 * C * 3 * C),
             "gemm_mfma_tape_kernel<unsigned short>": ("tape projections, I also before GELU", "F", 2 * C * 3 * C),
             "gemm_mfma_kernel<unsigned short>": ("forward projections (the forward timing)", None, None),
-            "stencil_mfma_kernel<float>": ("tape step, fp32 out", "B", 4 * C * 2 + C * 4),
+            "stencil_mfma_kernel<float>": ("tape step, fp32 out, loss sums (reads T)", "B", 5 * C * 2 + C * 4),
             "stencil_mfma_kernel<unsigned short>": ("forward step", "B", 5 * C * 2),
             "bw_loss_partial_kernel<unsigned short>": ("loss partials", "B", C * 4 + C * 2),
         }

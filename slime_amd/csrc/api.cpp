@@ -295,9 +295,11 @@ int run_project(slime_ca* h, const void* x, const float* x_scale, void* P, void*
 
 // S2-S6 plus the mass partials and S7 finalize: y_raw gets the unscaled output,
 // out_scale the per-(b, head) conservation factor.
+// loss_T, loss_part: the backward's tape step on the MFMA stencil (bf16, D = 64), which
+// also sums Y^2, Y T and T^2 per (b, head, tile) into loss_part (StencilArgs).
 int run_stencil(slime_ca* h, const void* x, const float* x_scale, const void* P, const void* I,
                 const void* V, void* y_raw, int y_f32, float* out_scale, hipStream_t s,
-                double* out_scale64 = nullptr) {
+                double* out_scale64 = nullptr, const void* loss_T = nullptr, double* loss_part = nullptr) {
     const slime_ca_config& c = h->cfg;
     StencilArgs a{};
     a.X = x;
@@ -322,6 +324,8 @@ int run_stencil(slime_ca* h, const void* x, const float* x_scale, const void* P,
     a.per_cell = c.growth_per_cell;
     a.dt = c.dt;
     a.growth_fn = c.growth_fn;
+    a.T = loss_T;
+    a.loss_part = loss_part;
     HIP_TRY(timed(h, h->stencil_ev, s, [&] { return launch_stencil(c.dtype, a, s); }));
     if (c.conservation == 1)
         HIP_TRY(launch_cell_conserve(c.dtype, x, x_scale, y_raw, y_f32, h->part_out, c.B, c.G, c.D, s));
@@ -832,7 +836,10 @@ int slime_ca_backward(slime_ca* h, const void* x_in, const void* target, float* 
         return fail(SLIME_EINVAL, "the backward supports the bell growth and global conservation only");
     const size_t C = h->C, BH = (size_t)c.B * c.H, n = (size_t)h->state_elems;
     const size_t cells = (size_t)c.B * c.G * c.G;
-    const int lchunks = backward_loss_chunks(c.G);
+    // bf16, D = 64: the tape step runs on the MFMA stencil, which sums the loss terms per
+    // tile itself (no loss-partial pass)
+    const bool loss_fused = c.dtype == 1 && c.D == 64;
+    const int lchunks = loss_fused ? h->tiles : backward_loss_chunks(c.G);
     const int nW = 1024;  // cell-pass workgroups per pod
     const long long rows_pod = (long long)(c.B / c.pods) * c.G * c.G;
     const int dw_chunks = backward_dw_chunks_per_pod(c.dtype, (int)C, rows_pod);
@@ -881,7 +888,8 @@ int slime_ca_backward(slime_ca* h, const void* x_in, const void* target, float* 
     if (rc) return rc;
     float* y32 = h->Sf ? h->Sf : h->bw_y32;
     float* rs = h->scale[0];
-    rc = run_stencil(h, x_in, nullptr, h->P, h->I, h->V, y32, 1, rs, s);
+    rc = run_stencil(h, x_in, nullptr, h->P, h->I, h->V, y32, 1, rs, s, nullptr,
+                     loss_fused ? target : nullptr, loss_fused ? h->bw_lpart : nullptr);
     if (rc) return rc;
 
     // backward through S7..S2 and the activations
@@ -908,6 +916,8 @@ int slime_ca_backward(slime_ca* h, const void* x_in, const void* target, float* 
     a.inv_n = (float)(1.0 / (double)n);
     a.lpart = h->bw_lpart;
     a.lchunks = lchunks;
+    a.loss_fused = loss_fused;
+    a.ysum_part = h->part_out;
     a.coef = h->bw_coef;
     a.loss_bh = h->bw_loss;
     a.gU = h->bw_gU;

@@ -175,29 +175,42 @@ __global__ __launch_bounds__(256) void bw_loss_partial_kernel(BackwardArgs a) {
 
 // One block per (b, head): fixed-order sums of the partials (strided per lane, then
 // a tree), then the S7 chain coefficients: gY = cY (gY' - cQ), and cQ is also the
-// uniform direct term of gX.
+// uniform direct term of gX. With loss_fused the partials are the tape stencil's
+// per-tile sums A = sum Y^2, B = sum Y T, C = sum T^2 and the mass partials' sum Y,
+// and with r = hi + lo: L = r^2 A - 2 r B + C, Q = (2 / N)(r A - B), each sum of
+// exact fp64 products, so only fp64 rounding separates them from the direct sums.
 __global__ __launch_bounds__(256) void bw_loss_finalize_kernel(BackwardArgs a) {
     const int bh = blockIdx.x;
-    __shared__ double s[3][256];
-    double l = 0.0, q = 0.0, bs = 0.0;
+    __shared__ double s[4][256];
+    double l = 0.0, q = 0.0, bs = 0.0, ys = 0.0;
     for (int c = threadIdx.x; c < a.lchunks; c += 256) {
         const double* p = a.lpart + ((long long)bh * a.lchunks + c) * 3;
         l += p[0];
         q += p[1];
         bs += p[2];
+        if (a.loss_fused) ys += a.ysum_part[(long long)bh * a.lchunks + c];
     }
     s[0][threadIdx.x] = l;
     s[1][threadIdx.x] = q;
     s[2][threadIdx.x] = bs;
+    s[3][threadIdx.x] = ys;
     __syncthreads();
     for (int w = 128; w > 0; w >>= 1) {
         if ((int)threadIdx.x < w)
 #pragma unroll
-            for (int k = 0; k < 3; ++k) s[k][threadIdx.x] += s[k][threadIdx.x + w];
+            for (int k = 0; k < 4; ++k) s[k][threadIdx.x] += s[k][threadIdx.x + w];
         __syncthreads();
     }
     if (threadIdx.x == 0) {
-        const double ls = s[0][0], qs = s[1][0], b_s = s[2][0];
+        double ls = s[0][0], qs = s[1][0], b_s = s[2][0];
+        if (a.loss_fused) {
+            const double r = (double)a.scale[bh] + (double)a.scale[gridDim.x + bh];
+            const double A = s[0][0], Bt = s[1][0], Ct = s[2][0];
+            const double N = (double)a.B * (double)a.G * (double)a.G * (double)(kHeads * a.D);
+            ls = __builtin_fma(r, __builtin_fma(r, A, -2.0 * Bt), Ct);
+            qs = (2.0 / N) * __builtin_fma(r, A, -Bt);
+            b_s = s[3][0];
+        }
         const bool guard = fabs(b_s) > 1e-6;
         a.coef[bh * 3 + 0] = guard ? a.scale[bh] : 1.0f;
         a.coef[bh * 3 + 1] = guard ? (float)(qs / b_s) : 0.0f;
@@ -1309,7 +1322,8 @@ template <typename T, int kD>
 hipError_t launch_dt(const BackwardArgs& a, hipStream_t s) {
     const long long cells = (long long)a.G * a.G;
     const long long n = (long long)a.B * cells * kHeads * kD;
-    hipLaunchKernelGGL((bw_loss_partial_kernel<T>), dim3(a.lchunks, a.B), dim3(256), 0, s, a);
+    if (!a.loss_fused)
+        hipLaunchKernelGGL((bw_loss_partial_kernel<T>), dim3(a.lchunks, a.B), dim3(256), 0, s, a);
     hipLaunchKernelGGL(bw_loss_finalize_kernel, dim3(a.B * kHeads), dim3(256), 0, s, a);
     if constexpr (sizeof(T) == 2 && kD == 64)  // G is a multiple of 8: whole cell pairs per row
         hipLaunchKernelGGL(bw_cell_ring_kernel, dim3(a.pods * a.nW), dim3(256), 0, s, a);

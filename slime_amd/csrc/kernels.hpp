@@ -81,6 +81,12 @@ struct StencilArgs {
     int B, G, D, per_pod, per_cell;
     float dt;
     int growth_fn;           // 0 bell, 1 Gaussian, 2 U exp(-U^2) (growth_args, stencil.hip)
+    // The backward's tape step only (bf16 state, D = 64, fp32 Y, bell growth): with T set
+    // the kernel also sums, per (b, head, tile), Y^2, Y T and T^2 of the stored Y and the
+    // target T [B][G][G][C] (storage type), each product exact in fp64, into
+    // loss_part [B][H][tiles][3] (the loss then needs no pass of its own over Y and T).
+    const void* T;
+    double* loss_part;
 };
 int stencil_tiles_per_batch(int G);
 // Host-side table for StencilArgs::kband: bytes for `pods` pods, and its contents
@@ -168,7 +174,13 @@ struct BackwardArgs {
     float inv_n;             // 1 / (B G^2 C)
     // work buffers
     double* lpart;           // [B*H][lchunks][3]
-    int lchunks;             // backward_loss_chunks(G)
+    int lchunks;             // backward_loss_chunks(G), or the stencil's tiles per batch when
+                             // loss_fused
+    // loss_fused: lpart holds the tape stencil's per-tile sums of Y^2, Y T, T^2 and
+    // ysum_part its per-tile sums of Y ([B*H][lchunks], the mass partials), from which
+    // the loss finalize forms the loss sums; no loss-partial pass runs.
+    int loss_fused;
+    const double* ysum_part;
     float* coef;             // [B*H][3]: gY = (coef0 + coef2) (gY' - coef1), coef0 + coef2 the
                              // scale r (or 1 under the guard); coef1 also enters gX
     double* loss_bh;         // [B*H] sum of squared errors

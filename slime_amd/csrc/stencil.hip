@@ -593,8 +593,9 @@ __host__ __device__ constexpr int nb_row(int c, int k) {
 }  // namespace mf
 
 // kGrowthFn: false for the bell growth; true for any of the three growth functions
-// through growth_args (one more multiply-add per value).
-template <typename TY, bool kGrowthFn>
+// through growth_args (one more multiply-add per value). kLoss (fp32 Y only): the
+// backward's tape step, which also sums Y^2, Y T and T^2 per (b, head, tile).
+template <typename TY, bool kGrowthFn, bool kLoss = false>
 __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilArgs a) {
     using namespace mf;
     constexpr int H = kHeads;
@@ -1028,8 +1029,13 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
         asm volatile("" : "+v"(pre[0]), "+v"(pre[1]), "+v"(pre[2]), "+v"(pre_band));
         TY* Yg = static_cast<TY*>(a.Y);
         float ysum[H];  // this lane's sum of stored Y per head
+        double lsum[3][kLoss ? H : 1];  // kLoss: this lane's Y^2, Y T, T^2 per head
 #pragma unroll
         for (int o = 0; o < H; ++o) ysum[o] = 0.f;
+        if constexpr (kLoss) {
+#pragma unroll
+            for (int o = 0; o < H; ++o) lsum[0][o] = lsum[1][o] = lsum[2][o] = 0.0;
+        }
         if constexpr (sizeof(TY) == 2) {
             // bf16: lanes grp and grp ^ 1 (lane ^ 16, the same cell) exchange one
             // 8-byte piece per head so that each stores 8 contiguous channels in one
@@ -1061,6 +1067,17 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
         } else {
             const long long base =
                 bbase + ((long long)(ty0 + cell / kTileX) * G + tx0 + cell % kTileX) * C + ch0;
+            // kLoss: the target at this lane's 4 x 2 channels of every head, all loads
+            // issued before the stores
+            uint2 tw[kLoss ? 2 : 1][kLoss ? H : 1];
+            if constexpr (kLoss) {
+                const bf16_t* Tg = static_cast<const bf16_t*>(a.T);
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                    for (int o = 0; o < H; ++o)
+                        tw[mb][o] = *reinterpret_cast<const uint2*>(Tg + base + o * kD + 16 * mb);
+            }
 #pragma unroll
             for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
@@ -1070,6 +1087,18 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
                     for (int e = 0; e < 4; ++e) {
                         r[e] = Store<TY>::round(y[o][mb][e]);
                         ysum[o] += r[e];
+                    }
+                    if constexpr (kLoss) {
+                        // products of an fp32 and a bf16 value are exact in fp64
+                        const float t4[4] = {bf16lo(tw[mb][o].x), bf16hi(tw[mb][o].x), bf16lo(tw[mb][o].y),
+                                             bf16hi(tw[mb][o].y)};
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const double yd = r[e], td = t4[e];
+                            lsum[0][o] = __builtin_fma(yd, yd, lsum[0][o]);
+                            lsum[1][o] = __builtin_fma(yd, td, lsum[1][o]);
+                            lsum[2][o] = __builtin_fma(td, td, lsum[2][o]);
+                        }
                     }
                     // fp32: 16-byte pieces per cell, plain stores, so L2 merges the
                     // pieces of each 128-byte line before it is written back.
@@ -1100,6 +1129,40 @@ __global__ __launch_bounds__(mf::kThreads, 2) void stencil_mfma_kernel(StencilAr
             double* dst = tid < H ? a.part_in : a.part_out;
             dst[((long long)b * H + j) * tpb + tile] = sum;
         }
+        if constexpr (kLoss) {
+            // The same butterflies over [Y^2 | Y T] and [T^2 | 0], the rows added through
+            // the last head's staging buffer: every wave has finished that head (the
+            // barrier above), the next tile's first loads fill the other buffer, and
+            // its first barrier follows these reads.
+            double r2[16], r3[16];
+#pragma unroll
+            for (int o = 0; o < H; ++o) {
+                r2[o] = lsum[0][o];
+                r2[H + o] = lsum[1][o];
+                r3[o] = lsum[2][o];
+                r3[H + o] = 0.0;
+            }
+            fold_half<8, 0x140>(r2, lane, 3);
+            fold_half<4, 0x141>(r2, lane, 2);
+            fold_half<2, 0x4E>(r2, lane, 1);
+            fold_half<1, 0xB1>(r2, lane, 0);
+            fold_half<8, 0x140>(r3, lane, 3);
+            fold_half<4, 0x141>(r3, lane, 2);
+            fold_half<2, 0x4E>(r3, lane, 1);
+            fold_half<1, 0xB1>(r3, lane, 0);
+            double* scr = reinterpret_cast<double*>(((gh - 1) & 1) ? bufB : bufA);
+            scr[tid] = r2[0];
+            scr[kThreads + tid] = r3[0];
+            __syncthreads();
+            if (tid < 3 * H) {
+                const int q = tid / H, j = tid % H;  // q: 0 Y^2, 1 Y T, 2 T^2
+                const double* src = scr + (q == 2 ? kThreads : 0) + (q == 1 ? H : 0) + j;
+                double sum = 0.0;
+#pragma unroll
+                for (int r = 0; r < kThreads / 16; ++r) sum += src[r * 16];
+                a.loss_part[(((long long)b * H + j) * tpb + tile) * 3 + q] = sum;
+            }
+        }
         if (t_next < 0) break;
         t_cur = t_next;
     }
@@ -1128,6 +1191,15 @@ hipError_t launch_mfma(const StencilArgs& a, hipStream_t s) {
     const int tiles = a.B * (a.G / kTileY) * (a.G / kTileX);
     const int grid = tiles < 2 * n_cu ? tiles : 2 * n_cu;  // two persistent workgroups per CU
     if (!a.sched) return hipErrorInvalidValue;
+    if (a.T) {  // the backward's tape step: fp32 Y and the bell growth only
+        if constexpr (std::is_same_v<TY, float>) {
+            if (a.growth_fn != 0 || !a.loss_part) return hipErrorInvalidValue;
+            hipLaunchKernelGGL((stencil_mfma_kernel<float, false, true>), dim3(grid), dim3(mf::kThreads), 0, s, a);
+            return hipGetLastError();
+        } else {
+            return hipErrorInvalidValue;
+        }
+    }
     if (a.growth_fn == 0)
         hipLaunchKernelGGL((stencil_mfma_kernel<TY, false>), dim3(grid), dim3(mf::kThreads), 0, s, a);
     else
