@@ -145,7 +145,9 @@ def _trace_work(workload: str) -> dict:
             "bw_dw_mfma2_kernel": ("weight gradients", "F", 2 * C * 3 * C),
             "gemm_mfma_tape_kernel<unsigned short>": ("tape projections, I also before GELU", "F", 2 * C * 3 * C),
             "gemm_mfma_kernel<unsigned short>": ("forward projections (the forward timing)", None, None),
-            "stencil_mfma_kernel<float>": ("tape step, fp32 out, loss sums (reads T)", "B", 5 * C * 2 + C * 4),
+            "stencil_mfma_kernel<float, false, true>": (
+                "tape step, fp32 out, loss sums (reads T)", "B", 5 * C * 2 + C * 4),
+            "stencil_mfma_kernel<float>": ("forward timing: last step, fp32 out", "B", 4 * C * 2 + C * 4),
             "stencil_mfma_kernel<unsigned short>": ("forward step", "B", 5 * C * 2),
             "bw_loss_partial_kernel<unsigned short>": ("loss partials", "B", C * 4 + C * 2),
         }
@@ -173,11 +175,12 @@ def _short_name(full: str) -> str:
     return name.split("(")[0].strip()
 
 
-def _work_key(name: str) -> str:
-    """The name with the boolean template arguments of a kernel's variants removed
-    (the growth-function instantiations do the same work per launch)."""
+def _work_key(name: str, work: dict) -> str:
+    """The key of `work` for a kernel: its full name when listed (variants whose work
+    differs), else the name with the boolean template arguments removed (the
+    growth-function instantiations do the same work per launch)."""
     import re
-    return re.sub(r", (true|false)", "", name)
+    return name if name in work else re.sub(r", (true|false)", "", name)
 
 
 def trace_summary(path: str, workload: str, cells: int = 0) -> str:
@@ -198,9 +201,9 @@ def trace_summary(path: str, workload: str, cells: int = 0) -> str:
              "work per launch | achieved | of peak |",
              "|---|---|---|---|---|---|---|---|---|---|---|"]
     for name, calls, avg, tot, pct, mn, mx in sorted(rows, key=lambda r: -r[3]):
-        if _work_key(name) not in work:
+        if _work_key(name, work) not in work:
             continue
-        what, kind, per_cell = work[_work_key(name)]
+        what, kind, per_cell = work[_work_key(name, work)]
         cols = [f"`{name}`", what, str(calls), f"{avg / 1e3:.1f}", f"{mn / 1e3:.1f}", f"{mx / 1e3:.1f}",
                 f"{tot / 1e6:.2f}", f"{pct:.2f}"]
         if kind == "B":

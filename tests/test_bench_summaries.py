@@ -99,3 +99,15 @@ def test_trace_summary_c4_counts_its_own_cells(bench, tmp_path):
     st = _row(bench.trace_summary(str(p), "c4"), "stencil_mfma_kernel")
     b = 5 * 512 * 2 * 16 * 128 * 128  # 16 pods x 128 x 128 cells
     assert st[8] == f"{b / 1e9:.3f} GB" and st[9] == f"{b / 0.5e-3 / 1e12:.2f} TB/s"
+
+
+def test_trace_summary_tells_the_loss_summing_tape_step_from_the_plain_fp32_step(bench, tmp_path):
+    p = tmp_path / "run_kernel_stats.csv"
+    pre = "void slime::(anonymous namespace)::stencil_mfma_kernel"
+    _write_stats(p, [(pre + "<float, false, true>(slime::StencilArgs)", 4, 1.0e6),
+                     (pre + "<float, false, false>(slime::StencilArgs)", 2, 1.0e6)])
+    s = bench.trace_summary(str(p), "c5")
+    tape, plain = _row(s, "<float, false, true>"), _row(s, "<float, false, false>")
+    C, cells = 512, 1 << 20
+    assert tape[8] == f"{(5 * C * 2 + C * 4) * cells / 1e9:.3f} GB"  # reads T as well
+    assert plain[8] == f"{(4 * C * 2 + C * 4) * cells / 1e9:.3f} GB"
