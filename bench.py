@@ -223,8 +223,8 @@ def trace_summary(path: str, workload: str, cells: int = 0) -> str:
 
 # ---- rocprofv3 --pmc HBM traffic summaries ------------------------------------------
 # The kernels whose traffic bench.py reports, keyed as pmc_traffic.json keys them, with
-# the short names of their workload's launches.
-_TRAFFIC_KERNELS = {"c3": {"stencil": "stencil_mfma_kernel<unsigned short, false>",
+# the short names of their workload's launches (boolean template arguments removed).
+_TRAFFIC_KERNELS = {"c3": {"stencil": "stencil_mfma_kernel<unsigned short>",
                            "gemm": "gemm_mfma_kernel<unsigned short>"}}
 
 
@@ -268,9 +268,10 @@ def traffic_summary(root: str, workload: str = "c3") -> tuple:
         rd, wr = fetch[k][0] * f_fac * 1024, write[k][0] * w_fac * 1024
         lines.append(f"| `{k}` | {fetch[k][1]} | {fetch[k][0]:,.0f} | {write[k][0]:,.0f} | "
                      f"{rd / 1e9:.3f} | {wr / 1e9:.3f} | {(rd + wr) / 1e9:.3f} |")
-        if k in names:
-            out[names[k]] = {"read_bytes": round(rd), "write_bytes": round(wr),
-                             "bytes_per_launch": round(rd + wr)}
+        kk = _work_key(k, {})
+        if kk in names:
+            out[names[kk]] = {"read_bytes": round(rd), "write_bytes": round(wr),
+                              "bytes_per_launch": round(rd + wr)}
     return "\n".join(lines), {workload: out}
 
 

@@ -76,7 +76,8 @@ def _write_pmc(dirpath, counter, rows):
 
 
 def test_traffic_summary_scales_by_the_calibration_copy(bench, tmp_path):
-    st = "void slime::(anonymous namespace)::stencil_mfma_kernel<unsigned short, false>(slime::StencilArgs)"
+    # the kernel's name carries its variant arguments (growth function, loss sums)
+    st = "void slime::(anonymous namespace)::stencil_mfma_kernel<unsigned short, false, false>(slime::StencilArgs)"
     gm = "void slime::(anonymous namespace)::gemm_mfma_kernel<unsigned short>(slime::GemmArgs)"
     # two dispatches each (the mean is taken), in two SE rows for one dispatch of the copy
     _write_pmc(tmp_path / "p_FETCH_SIZE", "FETCH_SIZE", [(st, 1000.0), (st, 3000.0), (gm, 500.0), (gm, 500.0)])
