@@ -1,5 +1,5 @@
 // ca_binding.cpp — a compiled C++ host of libslime_ca.so, written as the reference's
-// runtime would call it (the binding of INTEGRATION.md section 2): the organism's CA
+// runtime would call it (the binding a maintainer of the reference would add): the organism's CA
 // engine is created next to the organism, its weights are the reference's per-head
 // tensors embedded as dense matrices, and each generation calls
 // slime_neural_ca_update from the host instead of the device-side launch of
